@@ -1,0 +1,66 @@
+"""ctypes binding of libglm53_hip.so (the C ABI declared in include/glm53.h).
+
+Loading the library does not touch the GPU.  If the library is missing the
+import fails loudly: there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libglm53_hip.so"
+ABI_VERSION = 1
+
+EXPORTED = (
+    "glm53_abi_version",
+    "glm53_error_string",
+    "glm53_store_int8",
+    "glm53_sparse_mla_workspace_bytes",
+    "glm53_sparse_mla",
+    "glm53_moe_align_small",
+)
+
+_lib = None
+
+
+def load():
+    """Return the loaded library, raising if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is missing: build the HIP kernels first "
+            "(python glm-5.3-kernels_amd/build_lib.py or __graft_entry__.build())")
+    L = ctypes.CDLL(str(LIB_PATH))
+    P, I64, I, D = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double
+    L.glm53_abi_version.restype = I
+    L.glm53_abi_version.argtypes = []
+    L.glm53_error_string.restype = ctypes.c_char_p
+    L.glm53_error_string.argtypes = [I]
+    L.glm53_store_int8.restype = I
+    L.glm53_store_int8.argtypes = [P, I64, P, I64, I64, I64, I64, P, I, I64, P]
+    L.glm53_sparse_mla_workspace_bytes.restype = I64
+    L.glm53_sparse_mla_workspace_bytes.argtypes = [I64, I64, I64]
+    L.glm53_sparse_mla.restype = I
+    L.glm53_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, I64, P, I64,
+                                   P, I64, I64, P]
+    L.glm53_moe_align_small.restype = I
+    L.glm53_moe_align_small.argtypes = [P, I, I64, P, P, P, P]
+    version = L.glm53_abi_version()
+    if version != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH} has ABI version {version}, expected {ABI_VERSION}")
+    _lib = L
+    return L
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().glm53_error_string(rc).decode(errors="replace")
+        raise RuntimeError(f"{what} failed: {msg} (code {rc})")
+
+
+def stream_handle(device) -> int:
+    import torch
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,142 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Sparse NoPE MLA attention over the per-token INT8 cache, MI355X HIP kernels.
+
+Drop-in for `triton_mla_sparse_attention` of kernels/titan_mla.py:452-581
+(same name, signature, assertions and return value).  The kernels live in
+csrc/sparse_mla.hip behind glm53_sparse_mla; they run on the caller's
+current stream without host synchronisation, so the call is
+graph-capturable.  Output and split workspace come from torch's caching
+allocator.
+
+Cache rows are 528 bytes: 512 int8 latents, fp32 scale at byte 512, zero
+padding; the latent serves as both K and V (NoPE, one KV head).  The RoPE
+(dim_qk = 576) and BF16-cache branches the reference inherits are not part of
+its tested contract and are not provided here.
+"""
+import functools
+
+import torch
+
+import _glm53_lib as _lib
+
+LOG2E = 1.4426950408889634
+LOGE2 = 0.6931471805599453
+
+_BLOCK_DMODEL = 512
+_BLOCK_DPE = 64
+_BLOCK_DV = 512
+_DIM_QK = _BLOCK_DMODEL + _BLOCK_DPE  # 576
+_BLOCK_H = 16
+_ROW_BYTES = 528
+# Smallest tile width of the reference's autotune space: top-k must be a
+# multiple of it (kernels/titan_mla.py:45-49, :485-488).
+_MIN_BLOCK_N = 32
+KV_SPLITS_CANDIDATES = (1, 2, 4, 8, 16)
+_MIN_TOPK_PER_SPLIT = 128
+_SPLIT_MAX_OCCUPANCY = 4
+
+
+def num_compute_units(device_index):
+    return torch.cuda.get_device_properties(device_index).multi_processor_count
+
+
+def _next_power_of_2(n: int) -> int:
+    return 1 << (n - 1).bit_length() if n > 0 else 1
+
+
+@functools.lru_cache(maxsize=256)
+def _choose_num_kv_splits(num_tokens: int, num_head_groups: int, index_topk: int,
+                          sm_count: int) -> int:
+    """Power-of-2 split count that fills the device without dropping per-split
+    work below _MIN_TOPK_PER_SPLIT indices; 1 when the single-pass grid already
+    covers a quarter of the compute units (kernels/titan_mla.py:432-449)."""
+    baseline = num_tokens * num_head_groups
+    if baseline == 0 or baseline * _SPLIT_MAX_OCCUPANCY >= sm_count:
+        return 1
+    ideal = _next_power_of_2(max(1, index_topk // _MIN_TOPK_PER_SPLIT))
+    max_splits = max(1, sm_count // baseline)
+    max_splits = 1 << (max_splits.bit_length() - 1)
+    num_kv_splits = min(ideal, max_splits)
+    while num_kv_splits > 1 and index_topk % num_kv_splits != 0:
+        num_kv_splits //= 2
+    return max(1, num_kv_splits)
+
+
+def triton_mla_sparse_attention(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    indices: torch.Tensor,
+    sm_scale: float,
+    num_kv_splits: int | None = None,
+    sm_count: int | None = None,
+) -> torch.Tensor:
+    """Sparse MLA attention over top-k indices.
+
+    Args:
+        q:         [num_tokens, num_heads_q, 512] bf16
+        kv:        [seq_kv, 1, 528] int8 packed cache rows
+        indices:   [num_tokens, 1, topk] int32; entries outside [0, seq_kv)
+                   are masked
+        sm_scale:  softmax scale
+        num_kv_splits: None/0 = heuristic, 1 = single pass, n = n splits
+        sm_count:  compute-unit count for the heuristic (queried if None)
+
+    Returns:
+        out: [num_tokens, num_heads_q, 512] bf16
+    """
+    num_tokens, num_heads_q, dim_qk = q.shape
+    assert dim_qk in (_BLOCK_DMODEL, _DIM_QK), (
+        f"sparse MLA kernel requires dim_qk={_BLOCK_DMODEL} (NoPE) or "
+        f"{_DIM_QK} (RoPE), got {dim_qk}"
+    )
+    assert kv.shape[1] == 1 and kv.shape[2] == (_ROW_BYTES if kv.dtype == torch.int8 else dim_qk)
+    index_topk = indices.shape[2]
+    assert index_topk % _MIN_BLOCK_N == 0, (
+        f"topk ({index_topk}) must be a multiple of the smallest autotune "
+        f"BLOCK_N ({_MIN_BLOCK_N})"
+    )
+    if dim_qk != _BLOCK_DMODEL or kv.dtype != torch.int8:
+        raise NotImplementedError("only the NoPE INT8-cache path (dim_qk=512, 528-byte rows) is built")
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"q must be bf16, got {q.dtype}")
+
+    num_head_groups = triton_cdiv(num_heads_q, min(_BLOCK_H, num_heads_q))
+    if num_kv_splits is None or num_kv_splits == 0:
+        if sm_count is None:
+            sm_count = num_compute_units(q.device.index)
+        num_kv_splits = _choose_num_kv_splits(num_tokens, num_head_groups, index_topk, sm_count)
+    if num_kv_splits < 1:
+        raise ValueError(f"num_kv_splits must be >= 1, got {num_kv_splits}")
+
+    out = torch.empty((num_tokens, num_heads_q, _BLOCK_DV), dtype=torch.bfloat16, device=q.device)
+    if num_tokens == 0:
+        return out
+
+    if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    if indices.dtype != torch.int32:
+        # Out-of-range wide indices stay masked after narrowing.
+        valid = (indices >= 0) & (indices < kv.shape[0])
+        indices = torch.where(valid, indices, torch.full_like(indices, -1)).to(torch.int32)
+    if indices.stride(2) != 1:
+        indices = indices.contiguous()
+
+    L = _lib.load()
+    ws_bytes = L.glm53_sparse_mla_workspace_bytes(num_tokens, num_heads_q, num_kv_splits)
+    workspace = (torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None)
+    with torch.cuda.device(q.device):
+        rc = L.glm53_sparse_mla(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            kv.data_ptr(), kv.stride(0), kv.shape[0],
+            indices.data_ptr(), indices.stride(0),
+            num_tokens, num_heads_q, index_topk,
+            float(sm_scale), num_kv_splits,
+            workspace.data_ptr() if workspace is not None else None, ws_bytes,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.stream_handle(q.device))
+    _lib.check(rc, "glm53_sparse_mla")
+    return out
+
+
+def triton_cdiv(a: int, b: int) -> int:
+    return (a + b - 1) // b

@@ -1,0 +1,114 @@
+/*
+ * glm53.h -- C ABI of libglm53_hip.so, the MI355X (gfx950) kernels behind
+ * the GLM-5.3 decode hot path.
+ *
+ * Every entry point takes device pointers, element or byte strides and a
+ * HIP stream (hipStream_t passed as void*), enqueues its kernels on that
+ * stream and returns 0 on success.  Nothing here allocates device memory,
+ * synchronises the stream or reads device data on the host, so every call
+ * may be captured into a HIP graph.  A negative return is an argument error
+ * (see glm53_error_string); a positive return is the hipError_t of a failed
+ * launch.  No torch or HIP types appear in the signatures.
+ */
+#ifndef GLM53_H_
+#define GLM53_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLM53_ABI_VERSION 1
+
+/* Argument errors (negative return codes). */
+#define GLM53_ERR_NULL_POINTER   (-1)
+#define GLM53_ERR_BAD_SHAPE      (-2)
+#define GLM53_ERR_MISALIGNED     (-3)
+#define GLM53_ERR_WORKSPACE      (-4)
+#define GLM53_ERR_BAD_DTYPE      (-5)
+
+int glm53_abi_version(void);
+const char* glm53_error_string(int code);
+
+/*
+ * Per-token symmetric INT8 latent writer.
+ * Replaces the launch of _store_int8 in store_int8 (kernels/titan_kv.py:23-28;
+ * kernel body kernels/titan_kv.py:7-21).
+ *
+ * For each i in [0, n_slots): slot = slots[i]; if slot >= 0 the 528-byte row
+ * at cache + (slot / block_size) * cache_stride_block
+ *             + (slot % block_size) * cache_stride_slot
+ * receives 512 int8 values q = clamp(rint(x / s), -127, 127) with
+ * s = max(max|x| / 127, 1e-12) in IEEE fp32, then s as fp32 at byte 512 and
+ * zeros in bytes 516..527.  x is bf16 row i (x + i * x_row_stride elements,
+ * 512 contiguous values).  A negative slot leaves the cache untouched, and so
+ * does a slot >= capacity (the number of slots the cache holds; the
+ * reference leaves out-of-range positive slots undefined).
+ *   slots_is_i64: 1 for int64 slots, 0 for int32 slots.
+ *   cache strides are in bytes.
+ */
+int glm53_store_int8(const void* x, int64_t x_row_stride,
+                     void* cache, int64_t cache_stride_block,
+                     int64_t cache_stride_slot, int64_t block_size,
+                     int64_t capacity, const void* slots, int slots_is_i64,
+                     int64_t n_slots, void* stream);
+
+/*
+ * Sparse NoPE MLA attention over top-k indices into the 528-byte INT8 cache.
+ * Replaces the kernel launches of triton_mla_sparse_attention
+ * (kernels/titan_mla.py:500-581: _sparse_mla_kernel_final,
+ * _sparse_mla_kernel_split and _sparse_mla_merge_kernel).
+ *
+ *   q        bf16 [num_tokens, num_heads, 512], strides sq_t, sq_h (elements),
+ *            last dim contiguous, 16-byte aligned rows.
+ *   kv       528-byte rows, row r at kv + r * skv_t bytes (skv_t % 16 == 0),
+ *            seq_kv rows; only the first 528 bytes of a row are read.
+ *   indices  int32 [num_tokens, topk] with row stride si_t (elements); an
+ *            index outside [0, seq_kv) is masked out.
+ *   sm_scale softmax scale; logits are q.k * scale_j * fp32(sm_scale*log2 e)
+ *            in base 2, as the reference computes them.
+ *   num_splits  >= 1; the top-k axis is cut into num_splits slices of
+ *            ceil(topk / num_splits) indices whose partial results are merged
+ *            by log-sum-exp.  1 = single pass.
+ *   workspace   device scratch of glm53_sparse_mla_workspace_bytes(...)
+ *            bytes (unused when num_splits == 1; may then be NULL).
+ *   out      bf16 [num_tokens, num_heads, 512], strides so_t, so_h.
+ * A query whose indices are all masked produces exactly 0.
+ */
+int64_t glm53_sparse_mla_workspace_bytes(int64_t num_tokens, int64_t num_heads,
+                                         int64_t num_splits);
+int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h,
+                     const void* kv, int64_t skv_t, int64_t seq_kv,
+                     const int32_t* indices, int64_t si_t,
+                     int64_t num_tokens, int64_t num_heads, int64_t topk,
+                     double sm_scale, int64_t num_splits,
+                     void* workspace, int64_t workspace_bytes,
+                     void* out, int64_t so_t, int64_t so_h,
+                     void* stream);
+
+/*
+ * Stable MoE route alignment for 1..8 tokens, top-8 routing, 288 experts,
+ * block size 8, invalid routes ignored.
+ * Replaces the launch of _align_small in titan_moe_align_small
+ * (kernels/titan_moe_align.py:49-81; kernel body :12-46).
+ *
+ *   topk_ids  int32 or int64 (ids_is_i64) [num_routes], num_routes in [1, 64]
+ *   sorted_ids  int32 [num_routes * 8]: flat route ids grouped by expert in
+ *               ascending expert order, stable within an expert, each
+ *               expert padded to a multiple of 8 with num_routes; the tail
+ *               is num_routes as well.
+ *   expert_ids  int32 [num_routes]: expert of each 8-block, then -1.
+ *   num_tokens_post_padded  int32 [1]: sum over experts of ceil8(count).
+ * Routes outside [0, 288) (compared at full 64-bit width) are dropped.
+ */
+int glm53_moe_align_small(const void* topk_ids, int ids_is_i64,
+                          int64_t num_routes, int32_t* sorted_ids,
+                          int32_t* expert_ids,
+                          int32_t* num_tokens_post_padded, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLM53_H_ */

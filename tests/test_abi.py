@@ -1,0 +1,132 @@
+"""CPU checks of the drop-in boundary: the C ABI library loads and exports what
+include/glm53.h declares, host-side argument errors, and the Python
+contract errors of the three reference entry points.  No kernel is launched."""
+import ctypes
+import re
+import sys
+import types
+from pathlib import Path
+from unittest.mock import patch
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "glm53.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(glm53_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    import _glm53_lib
+    lib = _glm53_lib.load()
+    names = declared_functions()
+    assert set(names) == set(_glm53_lib.EXPORTED)
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.glm53_abi_version() == 1
+
+
+def test_host_side_argument_errors():
+    import _glm53_lib
+    L = _glm53_lib.load()
+    fake = ctypes.c_void_p(0x10000)   # never dereferenced: every call below fails validation
+    assert L.glm53_moe_align_small(None, 0, 8, None, None, None, None) == -1
+    assert L.glm53_moe_align_small(fake, 0, 0, fake, fake, fake, None) == -2
+    assert L.glm53_moe_align_small(fake, 0, 65, fake, fake, fake, None) == -2
+    assert L.glm53_store_int8(fake, 512, fake, 135168, 528, 256, 1024, fake, 1, -1, None) == -2
+    assert L.glm53_store_int8(fake, 512, fake, 135168, 528, 0, 1024, fake, 1, 4, None) == -2
+    assert L.glm53_store_int8(None, 512, fake, 135168, 528, 256, 1024, fake, 1, 4, None) == -1
+    assert L.glm53_store_int8(fake, 512, fake, 135168, 528, 256, 1024, fake, 1, 0, None) == 0
+    # misaligned q / row stride
+    mis = ctypes.c_void_p(0x10008)
+    assert L.glm53_sparse_mla(mis, 8192, 512, fake, 528, 10, fake, 2176, 1, 16, 2176, 0.04, 1,
+                              None, 0, fake, 8192, 512, None) == -3
+    assert L.glm53_sparse_mla(fake, 8192, 512, fake, 520, 10, fake, 2176, 1, 16, 2176, 0.04, 1,
+                              None, 0, fake, 8192, 512, None) == -3
+    # split path without workspace
+    assert L.glm53_sparse_mla(fake, 8192, 512, fake, 528, 10, fake, 2176, 1, 16, 2176, 0.04, 4,
+                              None, 0, fake, 8192, 512, None) == -4
+    assert L.glm53_sparse_mla(fake, 8192, 512, fake, 528, 10, fake, 2176, 0, 16, 2176, 0.04, 4,
+                              None, 0, fake, 8192, 512, None) == 0
+    assert L.glm53_sparse_mla_workspace_bytes(1, 16, 1) == 0
+    assert L.glm53_sparse_mla_workspace_bytes(2, 16, 4) == 2 * 4 * 16 * (512 * 4 + 4)
+    assert L.glm53_sparse_mla_workspace_bytes(1, 20, 2) == 2 * 32 * (512 * 4 + 4)
+    for code in (0, -1, -2, -3, -4, -5):
+        assert L.glm53_error_string(code)
+
+
+def test_moe_contract_errors_on_cpu():
+    import torch
+    from titan_moe_align import titan_moe_align_small
+    ok = torch.zeros(2, 8, dtype=torch.int32)
+    bad_cases = [
+        (torch.zeros(16, dtype=torch.int32), {}),           # ndim
+        (torch.zeros(9, 8, dtype=torch.int32), {}),         # B > 8
+        (torch.zeros(0, 8, dtype=torch.int32), {}),         # B < 1
+        (torch.zeros(2, 4, dtype=torch.int32), {}),         # top-k
+        (ok, {"block_size": 16}),
+        (ok, {"num_experts": 256}),
+        (ok, {"expert_map": ok}),
+        (ok, {"ignore_invalid_experts": False}),
+        (ok, {}),                                           # CPU tensor
+    ]
+    for ids, kw in bad_cases:
+        with pytest.raises(ValueError):
+            titan_moe_align_small(ids, **kw)
+
+
+def test_mla_and_writer_contract_assertions_on_cpu():
+    import torch
+    from titan_kv import store_int8
+    from titan_mla import triton_mla_sparse_attention, _choose_num_kv_splits
+    kv = torch.zeros(256, 1, 528, dtype=torch.int8)
+    q = torch.zeros(1, 16, 512, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 1, 2176, dtype=torch.int32)
+    with pytest.raises(AssertionError):
+        triton_mla_sparse_attention(torch.zeros(1, 16, 256, dtype=torch.bfloat16), kv, idx, 0.04)
+    with pytest.raises(AssertionError):
+        triton_mla_sparse_attention(q, torch.zeros(256, 1, 512, dtype=torch.int8), idx, 0.04)
+    with pytest.raises(AssertionError):
+        triton_mla_sparse_attention(q, kv, torch.zeros(1, 1, 100, dtype=torch.int32), 0.04)
+    with pytest.raises(NotImplementedError):
+        triton_mla_sparse_attention(torch.zeros(1, 16, 576, dtype=torch.bfloat16),
+                                    torch.zeros(256, 1, 576, dtype=torch.bfloat16), idx, 0.04)
+    with pytest.raises(AssertionError):
+        store_int8(torch.zeros(4, 256, dtype=torch.bfloat16), torch.zeros(1, 256, 528, dtype=torch.uint8),
+                   torch.arange(4))
+    with pytest.raises(AssertionError):
+        store_int8(torch.zeros(4, 512, dtype=torch.bfloat16), torch.zeros(1, 256, 528, dtype=torch.uint8),
+                   torch.arange(5))
+    assert [_choose_num_kv_splits(t, 1, 2176, 70) for t in (1, 6, 8, 2048)] == [32, 8, 8, 1]
+
+
+def test_import_does_not_touch_cuda():
+    """Mirrors tests/test_cpu_contracts.py:33-53: importing the entry-point
+    modules must not query the device."""
+    fake_torch = types.ModuleType("torch")
+    fake_torch.Tensor = object
+
+    class NoCUDA:
+        def __getattr__(self, name):
+            raise AssertionError(f"import-time torch.cuda access: {name}")
+
+    fake_torch.cuda = NoCUDA()
+    import importlib.util
+    pkg = ROOT / "glm-5.3-kernels_amd"
+    with patch.dict(sys.modules, {"torch": fake_torch}):
+        for fname, exported in (("titan_kv.py", "store_int8"),
+                                ("titan_mla.py", "triton_mla_sparse_attention"),
+                                ("titan_moe_align.py", "titan_moe_align_small")):
+            spec = importlib.util.spec_from_file_location("isolated_" + fname[:-3], pkg / fname)
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            assert callable(getattr(mod, exported))
+
+
+def test_product_does_not_import_oracle():
+    for f in (ROOT / "glm-5.3-kernels_amd").rglob("*.py"):
+        text = f.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, f

@@ -1,0 +1,222 @@
+"""GPU parity of triton_mla_sparse_attention (HIP) against the CPU oracle.
+
+Bar (BF16 attention output): max-abs <= 2e-2 and mean-abs <= 2e-3 against the
+oracle's faithful restatement run with the same split count and tile width;
+plus the reference's own statistical checks against fp32 attention over the
+original BF16 latents (tests/verify_mla.py:71-94)."""
+import numpy as np
+import pytest
+import torch
+
+import workloads as W
+from conftest import log_case
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 2e-3
+
+
+def u16(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def rows_np(cache):
+    return cache.contiguous().view(torch.uint8).cpu().numpy().reshape(-1, 528)
+
+
+def f32(u):
+    from oracle import bf16_to_f32
+    return bf16_to_f32(u)
+
+
+def bf16_ulp(v):
+    """Spacing of bf16 values at |v| (8 significant bits)."""
+    a = np.maximum(np.abs(v), np.float32(2.0 ** -126))
+    return np.exp2(np.floor(np.log2(a)) - 7)
+
+
+def compare(out, want_u16, tag):
+    got = out.float().cpu().numpy()
+    want = f32(want_u16)
+    err = np.abs(got - want)
+    ulps = err / bf16_ulp(want)
+    print(f"[cmp] {tag}: max|ref| {np.abs(want).max():.3g} max-abs {err.max():.3g} "
+          f"mean-abs {err.mean():.3g} max-ulp {ulps.max():.3g}", flush=True)
+    assert np.isfinite(got).all(), tag
+    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (tag, float(err.max()), float(err.mean()))
+    return float(err.max()), float(err.mean())
+
+
+def textbook_check(out, ref64, tag):
+    """Against float64 softmax attention over the dequantised rows: relative
+    bars (the bf16 output and bf16(p * scale) operand carry 2^-9 relative
+    rounding, so heavy-tailed rows make absolute errors scale with |out|)."""
+    got = out.float().cpu().numpy().astype(np.float64)
+    nmse = ((got - ref64) ** 2).sum() / (ref64 ** 2).sum()
+    cos = (got * ref64).sum() / np.sqrt((got ** 2).sum() * (ref64 ** 2).sum())
+    print(f"[f64] {tag}: nmse {nmse:.3g} cos {cos:.8f}", flush=True)
+    assert nmse < 1e-4 and cos > 0.99995, (tag, nmse, cos)
+
+
+@pytest.fixture(scope="module")
+def small_cache(cuda, oracle):
+    from titan_kv import store_int8
+    w = W.writer_small(cuda, seed=W.SEED_FIXTURE)
+    store_int8(w["x"], w["cache"], w["slots"])
+    torch.cuda.synchronize()
+    return w, rows_np(w["cache"])
+
+
+@pytest.mark.parametrize("splits", [1, 2, 4, 8, 16, 17, 32, 68, 100])
+def test_small_b1_splits(cuda, oracle, small_cache, splits):
+    from titan_mla import triton_mla_sparse_attention
+    w, rows = small_cache
+    log_case("mla small B1 splits", splits)
+    n = w["n_rows"]
+    out = triton_mla_sparse_attention(w["q"], w["cache"].view(n, 1, 528), w["idx"], W.SM_SCALE,
+                                      num_kv_splits=splits)
+    torch.cuda.synchronize()
+    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=splits)
+    mx, mean = compare(out, want, f"splits={splits}")
+    assert mx <= 2 ** -7 and mean < 1e-4        # ~bf16 ulp-level agreement
+
+
+def test_small_auto_splits_and_graph(cuda, oracle, small_cache):
+    from titan_mla import triton_mla_sparse_attention, _choose_num_kv_splits
+    w, rows = small_cache
+    log_case("mla small auto + graph")
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    out = triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE)
+    s = _choose_num_kv_splits(1, 1, 2176, torch.cuda.get_device_properties(0).multi_processor_count)
+    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=s)
+    compare(out, want, "auto")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout = triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gout, out)
+
+
+def test_reference_verify_protocol(cuda):
+    """tests/verify_mla.py:71-94 at 65536 rows: B in {1, 6, 8}, q x 0.15,
+    partial -1 padding, a positive out-of-range index; fp32 attention over the
+    ORIGINAL bf16 latents; NMSE < 1e-3, cosine > 0.999; all -1 -> exactly 0."""
+    from titan_kv import store_int8
+    from titan_mla import triton_mla_sparse_attention
+    n = 65536
+    g = W.gen(cuda, W.SEED_FIXTURE)
+    orig = torch.randn(n, 512, device=cuda, dtype=torch.bfloat16, generator=g)
+    orig[:, :128] *= 0.05
+    orig[:, 256:384] *= 8
+    orig[0] = 0
+    cache = torch.zeros(n // 256, 256, 528, device=cuda, dtype=torch.int8)
+    store_int8(orig, cache, torch.arange(n, device=cuda, dtype=torch.int64))
+    kv = cache.view(n, 1, 528)
+    for batch in (1, 6, 8):
+        q = torch.randn(batch, 16, 512, generator=g, device=cuda, dtype=torch.bfloat16) * 0.15
+        idx = torch.randint(n, (batch, 1, 2176), generator=g, device=cuda, dtype=torch.int32)
+        idx[:, :, 2048:] = -1
+        if batch > 1:
+            idx[1, :, 2000:] = -1
+        idx[0, 0, 0] = n + 5
+        valid = (idx[:, 0] >= 0) & (idx[:, 0] < n)
+        chosen = orig[idx[:, 0].clamp(0, n - 1).long()].float()
+        chosen.masked_fill_(~valid[:, :, None], 0)
+        logits = torch.bmm(q.float(), chosen.transpose(1, 2).contiguous()) * (512 ** -0.5)
+        logits.masked_fill_(~valid[:, None, :], -float("inf"))
+        ref = torch.bmm(logits.softmax(-1), chosen)
+        for splits in (1, 4, 8, 16, None):
+            log_case("mla verify protocol", batch, splits)
+            out = triton_mla_sparse_attention(q, kv, idx, 512 ** -0.5, num_kv_splits=splits)
+            nmse = ((out.float() - ref).square().sum() / ref.square().sum()).item()
+            cos = torch.nn.functional.cosine_similarity(out.float().flatten(), ref.flatten(), dim=0).item()
+            assert bool(torch.isfinite(out).all()) and nmse < 1e-3 and cos > 0.999, (batch, splits, nmse, cos)
+            blank = triton_mla_sparse_attention(q, kv, torch.full_like(idx, -1), 512 ** -0.5,
+                                                num_kv_splits=splits)
+            assert torch.equal(blank, torch.zeros_like(blank)), (batch, splits)
+
+
+def test_head_counts_and_edges(cuda, oracle, small_cache):
+    from titan_mla import triton_mla_sparse_attention
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    g = W.gen(cuda, 3)
+    for heads, topk, splits in ((8, 256, 1), (20, 256, 3), (32, 512, 4), (16, 32, 1), (16, 64, 5)):
+        log_case("mla heads/topk/splits", heads, topk, splits)
+        q = torch.randn(3, heads, 512, generator=g, device=cuda).to(torch.bfloat16)
+        idx = torch.randint(-50, n + 50, (3, 1, topk), generator=g, device=cuda, dtype=torch.int32)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+        torch.cuda.synchronize()
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits)
+        compare(out, want, (heads, topk, splits))
+    # int64 indices, including values that alias valid rows modulo 2^32
+    q = torch.randn(2, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+    idx64 = torch.randint(0, n, (2, 1, 256), generator=g, device=cuda, dtype=torch.int64)
+    idx64[0, 0, :40] += 1 << 32
+    out = triton_mla_sparse_attention(q, kv, idx64, W.SM_SCALE, num_kv_splits=2)
+    clean = torch.where((idx64 >= 0) & (idx64 < n), idx64, -1).to(torch.int32)
+    want = oracle.sparse_mla(u16(q), rows, clean.cpu().numpy(), W.SM_SCALE, n_splits=2)
+    compare(out, want, "int64")
+    # no tokens
+    empty = triton_mla_sparse_attention(q[:0], kv, idx64[:0].to(torch.int32), W.SM_SCALE)
+    assert empty.shape == (0, 16, 512)
+
+
+@pytest.fixture(scope="module")
+def full_cache(cuda):
+    from titan_kv import store_int8
+    g, x, cache, slots = W.decode_cache(cuda, seed=W.SEED_BENCH, dist="t3")
+    store_int8(x, cache, slots)
+    torch.cuda.synchronize()
+    del x
+    return g, cache
+
+
+@pytest.mark.slow
+def test_full_context_b1_b8(cuda, oracle, full_cache):
+    """262144-row cache: B=1 with 2048 uniform + 128 pads, B=8 locality-biased
+    with 0..256 pads per row (Student-t latents stress per-row scales)."""
+    from titan_mla import triton_mla_sparse_attention, _choose_num_kv_splits
+    g, cache = full_cache
+    n = cache.shape[0] * 256
+    kv = cache.view(n, 1, 528)
+    rows = rows_np(cache)
+    cu = torch.cuda.get_device_properties(0).multi_processor_count
+    for name, (q, idx) in (("b1", W.decode_b1_inputs(cuda, g)), ("b8", W.decode_b8_inputs(cuda, g))):
+        for splits in (None, 1, 8):
+            log_case("mla full context", name, splits)
+            out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+            torch.cuda.synchronize()
+            s = splits or _choose_num_kv_splits(q.shape[0], 1, 2176, cu)
+            want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s,
+                                     nthreads=oracle.default_threads())
+            compare(out, want, (name, splits))
+            ref64 = oracle.sparse_mla_f64(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE,
+                                          nthreads=oracle.default_threads())
+            textbook_check(out, ref64, (name, splits))
+
+
+@pytest.mark.slow
+def test_prefill_shaped_sampled(cuda, oracle, full_cache):
+    """T = 2048 query tokens, causal locality-biased indices; the oracle checks
+    a sample of 48 tokens (first, last and random)."""
+    from titan_mla import triton_mla_sparse_attention
+    g, cache = full_cache
+    n = cache.shape[0] * 256
+    kv = cache.view(n, 1, 528)
+    rows = rows_np(cache)
+    q, idx, _, _ = W.prefill_inputs(cuda, g)
+    log_case("mla prefill-shaped T=2048")
+    out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE)
+    torch.cuda.synchronize()
+    pick = np.unique(np.concatenate([[0, 1, 2047], np.random.default_rng(0).integers(0, 2048, 45)]))
+    qs = u16(q)[pick]
+    ids = idx.cpu().numpy()[pick]
+    want = oracle.sparse_mla(qs, rows, ids, W.SM_SCALE, n_splits=1, nthreads=oracle.default_threads())
+    got = out[torch.as_tensor(pick, device=cuda)]
+    compare(got, want, "prefill sample")

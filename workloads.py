@@ -1,0 +1,162 @@
+"""Seeded synthetic inputs for the decode hot path's benchmark configurations.
+
+Shared by tests/ and bench.py.  Everything is generated on the target device
+with a torch.Generator, so the same seed gives the same tensors on every run
+of the same build.  Seeds follow the reference's choices: 20260910 for
+fixtures (tests/verify_mla.py:107) and 37 for benchmarks (benchmarks/mla.py:27).
+
+Configurations (sizes as in the benchmark definition):
+  writer_small   store_int8 of 16384 N(0,1) rows into [64, 256, 528], slots arange;
+                 decode B=1 with 2176 indices uniform in [0, 16384), last 128 = -1
+  moe_small      routes [B, 8], 8 distinct experts per token from 288, B in {1,2,4,8}
+  decode_b1      262144 N(0,1) rows into [1024, 256, 528]; q [1, 16, 512];
+                 2048 indices uniform in [0, 262144) then 128 x -1
+  decode_b8      the same cache from Student-t(3) x 0.5 latents; q [8, 16, 512];
+                 per batch 0..256 trailing -1 pads, half of the valid indices in
+                 the last 4096 positions, half uniform
+  prefill_t2048  q [2048, 16, 512]; token t at position 260096 + t with 2176
+                 indices <= its position (half within 4096 behind it, half
+                 uniform); store_int8 of 2048 new rows to a random permutation
+                 of slots
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+SEED_FIXTURE = 20260910
+SEED_BENCH = 37
+LATENT = 512
+ROW_BYTES = 528
+BLOCK = 256
+TOPK = 2176
+HEADS = 16
+SM_SCALE = 512 ** -0.5
+
+
+def gen(device, seed):
+    return torch.Generator(device=device).manual_seed(seed)
+
+
+def student_t3(shape, g, device, dtype=torch.float32):
+    """Student-t with 3 degrees of freedom: z / sqrt(chi2_3 / 3)."""
+    z = torch.randn(shape, generator=g, device=device, dtype=dtype)
+    chi = torch.zeros(shape, device=device, dtype=dtype)
+    for _ in range(3):
+        chi += torch.randn(shape, generator=g, device=device, dtype=dtype) ** 2
+    return z / torch.sqrt(chi / 3)
+
+
+def latents(n, device, g, dist="normal", chunk=65536):
+    out = torch.empty(n, LATENT, device=device, dtype=torch.bfloat16)
+    for s in range(0, n, chunk):
+        e = min(n, s + chunk)
+        if dist == "normal":
+            out[s:e] = torch.randn(e - s, LATENT, generator=g, device=device)
+        else:
+            out[s:e] = student_t3((e - s, LATENT), g, device) * 0.5
+    return out
+
+
+def empty_cache(n_rows, device):
+    assert n_rows % BLOCK == 0
+    return torch.zeros(n_rows // BLOCK, BLOCK, ROW_BYTES, device=device, dtype=torch.int8)
+
+
+def uniform_indices(batch, n_rows, valid, device, g):
+    idx = torch.randint(n_rows, (batch, 1, TOPK), generator=g, device=device, dtype=torch.int32)
+    idx[:, :, valid:] = -1
+    return idx
+
+
+def local_biased_indices(batch, n_rows, device, g, max_pads=256, window=4096, positions=None):
+    """Per row b: pads_b ~ U{0..max_pads} trailing -1; of the valid entries half
+    fall in [pos_b - window + 1, pos_b] and half uniform in [0, pos_b]
+    (pos_b = n_rows - 1 unless positions are given), in random order."""
+    idx = torch.full((batch, 1, TOPK), -1, device=device, dtype=torch.int32)
+    pads = torch.randint(0, max_pads + 1, (batch,), generator=g, device=device)
+    pos = (torch.full((batch,), n_rows - 1, device=device, dtype=torch.int64)
+           if positions is None else positions.to(torch.int64))
+    lo = (pos - window + 1).clamp_min(0)
+    u1 = torch.rand(batch, TOPK, generator=g, device=device, dtype=torch.float64)
+    u2 = torch.rand(batch, TOPK, generator=g, device=device, dtype=torch.float64)
+    pick_local = torch.rand(batch, TOPK, generator=g, device=device) < 0.5
+    local = lo[:, None] + torch.floor(u1 * (pos - lo + 1)[:, None].to(torch.float64)).to(torch.int64)
+    unif = torch.floor(u2 * (pos + 1)[:, None].to(torch.float64)).to(torch.int64)
+    vals = torch.where(pick_local, local, unif).to(torch.int32)
+    keep = torch.arange(TOPK, device=device)[None, :] < (TOPK - pads)[:, None]
+    idx[:, 0, :] = torch.where(keep, vals, torch.full_like(vals, -1))
+    return idx
+
+
+def writer_small(device, seed=SEED_BENCH):
+    g = gen(device, seed)
+    n = 16384
+    x = latents(n, device, g)
+    cache = empty_cache(n, device)
+    slots = torch.arange(n, device=device, dtype=torch.int64)
+    q = torch.randn(1, HEADS, LATENT, generator=g, device=device).to(torch.bfloat16)
+    idx = uniform_indices(1, n, TOPK - 128, device, g)
+    return dict(x=x, cache=cache, slots=slots, q=q, idx=idx, n_rows=n)
+
+
+def decode_cache(device, seed=SEED_BENCH, dist="normal", n_rows=262144):
+    g = gen(device, seed)
+    x = latents(n_rows, device, g, dist)
+    cache = empty_cache(n_rows, device)
+    slots = torch.arange(n_rows, device=device, dtype=torch.int64)
+    return g, x, cache, slots
+
+
+def decode_b1_inputs(device, g, n_rows=262144):
+    q = torch.randn(1, HEADS, LATENT, generator=g, device=device).to(torch.bfloat16)
+    idx = uniform_indices(1, n_rows, 2048, device, g)
+    return q, idx
+
+
+def decode_b8_inputs(device, g, n_rows=262144):
+    q = torch.randn(8, HEADS, LATENT, generator=g, device=device).to(torch.bfloat16)
+    idx = local_biased_indices(8, n_rows, device, g)
+    return q, idx
+
+
+def prefill_inputs(device, g, n_rows=262144, tokens=2048):
+    q = torch.randn(tokens, HEADS, LATENT, generator=g, device=device).to(torch.bfloat16)
+    pos = n_rows - tokens + torch.arange(tokens, device=device)
+    idx = local_biased_indices(tokens, n_rows, device, g, max_pads=0, positions=pos)
+    new_rows = torch.randn(tokens, LATENT, generator=g, device=device).to(torch.bfloat16)
+    slots = torch.randperm(n_rows, generator=g, device=device)[:tokens]
+    return q, idx, new_rows, slots
+
+
+def moe_routes(batch, device, g, dtype=torch.int32):
+    """8 distinct experts per token drawn uniformly from 288."""
+    keys = torch.rand(batch, 288, generator=g, device=device)
+    return keys.argsort(dim=1)[:, :8].to(dtype).contiguous()
+
+
+# ----------------------------------------------------------------- bytes
+
+def writer_bytes(n_rows: int) -> int:
+    """Algorithmic bytes of store_int8: bf16 row in, int64 slot in, 528-B row out."""
+    return n_rows * (LATENT * 2 + 8 + ROW_BYTES)
+
+
+def mla_bytes(idx: torch.Tensor, n_rows: int, heads: int = HEADS) -> int:
+    """Gathered valid rows + indices + q + out (split partials not counted)."""
+    t = idx.shape[0]
+    valid = int(((idx >= 0) & (idx < n_rows)).sum().item())
+    return valid * ROW_BYTES + t * (idx.shape[-1] * 4 + 2 * heads * LATENT * 2)
+
+
+def mla_flops(idx: torch.Tensor, n_rows: int, heads: int = HEADS) -> int:
+    valid = int(((idx >= 0) & (idx < n_rows)).sum().item())
+    return 4 * heads * LATENT * valid
+
+
+def human(n: float) -> str:
+    return f"{n:.3g}"
+
+
+__all__ = [n for n in dir() if not n.startswith("_") and n not in ("math", "torch", "annotations")]
