@@ -1,0 +1,340 @@
+#!/usr/bin/env python3
+"""Benchmark of the GLM-5.3 decode hot path on one MI355X.
+
+Headline: sparse NoPE MLA decode at B=8 over a 262144-row INT8 cache with
+2176 indices per query (16 heads, one KV head).  A step is one call of
+triton_mla_sparse_attention; it is captured once in a HIP graph and replayed
+(the reference's protocol, benchmarks/mla.py:38-55): W untimed replays, then K
+timed replays bracketed by device synchronisation, timed with events on the
+stream the kernels run on; by default 10 steps are captured back to back in
+one graph (as decode steps sit inside one captured model step in serving;
+--unroll 1 gives the reference's one-call-per-replay figure, also reported).
+`value` is achieved algorithmic GB/s of the step
+(gathered valid 528-byte rows + indices + q + out) with inputs resident in
+HBM; warm = the replayed working set may sit in the 256 MB Infinity Cache, as
+in the reference's measurements; the cold figures flush it (a 1 GiB write)
+before every timed step.
+
+Extra fields: the B=1 decode, the 262144-row store_int8 writer, the MoE
+align (16 calls per graph, as docs/measurements.json:1445 records), the
+prefill-shaped T=2048 call, and the CPU baseline (the C oracle on the host
+cores, a bounded sample of the same workload).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+Prints one JSON line on stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "glm-5.3-kernels_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "sparse-MLA decode µs/step + achieved HBM GB/s, B1/B8, 262k ctx, 2176 idx"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """Events recorded on the current stream (the one the kernels use)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def replay_loop(self, graph, k: int) -> float:
+        torch = self.torch
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(k):
+            graph.replay()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) * 1e3 / k          # us per replay
+
+    def cold_loop(self, graph, k: int, flush) -> float:
+        torch = self.torch
+        evs = []
+        for _ in range(k):
+            flush()
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            graph.replay()
+            e.record()
+            evs.append((s, e))
+        torch.cuda.synchronize()
+        return statistics.median(s.elapsed_time(e) * 1e3 for s, e in evs)
+
+
+def capture(torch, fn, unroll: int = 1):
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(unroll):
+            out = fn()
+    torch.cuda.synchronize()
+    return g, out
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only: skip extras and CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--splits", type=int, default=None, help="force num_kv_splits for the decode calls")
+    ap.add_argument("--sweep", action="store_true",
+                    help="print a decode latency table over split counts (stderr) and exit")
+    ap.add_argument("--unroll", type=int, default=10,
+                    help="decode steps captured back to back per graph (K must be a multiple)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 256 MiB device copy (the HBM byte-counter calibration) and exit")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs the hot path at the per-rank shape on a "
+              "single MI355X; multi-GPU runs are not part of it.", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0 or args.unroll < 1 or args.steps % args.unroll:
+        ap.error("steps >= 1, warmup >= 0, steps a multiple of unroll")
+
+    import numpy as np
+    import torch
+
+    import workloads as W
+    from titan_kv import store_int8
+    from titan_mla import triton_mla_sparse_attention, _choose_num_kv_splits_mi355x
+    from titan_moe_align import titan_moe_align_small
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    props = torch.cuda.get_device_properties(dev)
+    cu = props.multi_processor_count
+    timer = Timer(torch)
+    flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+
+    def flush():
+        flush_buf.fill_(1)
+
+    K, Wm = args.steps, args.warmup
+    extra = {}
+
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(3)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 5 copies of 268435456 bytes")
+        return
+
+    # ---------------------------------------------------------------- caches
+    log("building 262144-row caches")
+    g8, x8, cache8, slots8 = W.decode_cache(dev, seed=W.SEED_BENCH, dist="t3")
+    store_int8(x8, cache8, slots8)
+    n_rows = cache8.shape[0] * W.BLOCK
+    kv8 = cache8.view(n_rows, 1, W.ROW_BYTES)
+    q8, idx8 = W.decode_b8_inputs(dev, g8)
+    del x8
+
+    if args.sweep:
+        g1s, x1s, cache1s, slots1s = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
+        store_int8(x1s, cache1s, slots1s)
+        del x1s
+        q1s, idx1s = W.decode_b1_inputs(dev, g1s)
+        kv1s = cache1s.view(n_rows, 1, W.ROW_BYTES)
+        for name, q_, kv_, idx_ in (("b1", q1s, kv1s, idx1s), ("b8", q8, kv8, idx8)):
+            for sp in (1, 2, 4, 8, 16, 17, 32, 34, 64, 68):
+                for unroll in (1, 10):
+                    gr, _ = capture(torch, lambda: triton_mla_sparse_attention(q_, kv_, idx_, W.SM_SCALE,
+                                                                               num_kv_splits=sp), unroll)
+                    for _ in range(10):
+                        gr.replay()
+                    us = timer.replay_loop(gr, 50) / unroll
+                    usc = timer.cold_loop(gr, 20, flush) / unroll
+                    log(f"sweep {name} splits={sp:3d} unroll={unroll:2d} warm {us:8.2f} us  cold {usc:8.2f} us")
+                    del gr
+        return
+
+    # ---------------------------------------------------------------- headline: B=8
+    def mla_b8():
+        return triton_mla_sparse_attention(q8, kv8, idx8, W.SM_SCALE, num_kv_splits=args.splits)
+
+    s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
+    graph8, _ = capture(torch, mla_b8, args.unroll)
+    for _ in range(Wm):
+        graph8.replay()
+    log(f"decode_b8: timing {K} steps (splits={s8}, {args.unroll} per graph)")
+    us8 = timer.replay_loop(graph8, K // args.unroll) / args.unroll
+    bytes8 = W.mla_bytes(idx8, n_rows)
+    gbs8 = bytes8 / (us8 * 1e-6) / 1e9
+    # the dominant kernel alone (first stage: split attention -> partials)
+    from titan_mla import sparse_mla_partials
+    pg, _ = capture(torch, lambda: sparse_mla_partials(q8, kv8, idx8, W.SM_SCALE, s8), args.unroll)
+    for _ in range(Wm):
+        pg.replay()
+    us8_kernel = timer.replay_loop(pg, K // args.unroll) / args.unroll
+    del pg
+    g8_1, _ = capture(torch, mla_b8, 1)
+    us8_cold = timer.cold_loop(g8_1, min(K, 50), flush)
+    us8_single = timer.replay_loop(g8_1, min(K, 100))
+    del g8_1
+    extra["decode_b8"] = {"us_per_step_warm": round(us8, 3), "us_per_step_cold": round(us8_cold, 3),
+                          "us_per_step_one_call_per_graph": round(us8_single, 3),
+                          "us_split_kernel_alone": round(us8_kernel, 3),
+                          "algorithmic_bytes": bytes8, "gbs_warm": round(gbs8, 1),
+                          "gbs_cold": round(bytes8 / (us8_cold * 1e-6) / 1e9, 1), "num_kv_splits": s8,
+                          "flops": W.mla_flops(idx8, n_rows)}
+
+    cpu = None
+    if not args.quick:
+        # ------------------------------------------------------------ B=1
+        g1, x1, cache1, slots1 = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
+        torch.cuda.synchronize()
+        # writer: 262144 rows, N(0,1) (the full-context writer configuration)
+        wg, _ = capture(torch, lambda: store_int8(x1, cache1, slots1))
+        for _ in range(max(1, Wm // 4)):
+            wg.replay()
+        log("store_int8 262144 rows")
+        us_w = timer.replay_loop(wg, max(5, K // 10))
+        us_w_cold = timer.cold_loop(wg, 10, flush)
+        wb = W.writer_bytes(x1.shape[0])
+        extra["store_int8_262144"] = {"us_per_call_warm": round(us_w, 2), "us_per_call_cold": round(us_w_cold, 2),
+                                      "algorithmic_bytes": wb, "gbs_warm": round(wb / (us_w * 1e-6) / 1e9, 1),
+                                      "gbs_cold": round(wb / (us_w_cold * 1e-6) / 1e9, 1),
+                                      "hbm_frac_cold": round(wb / (us_w_cold * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+        del wg
+        kv1 = cache1.view(n_rows, 1, W.ROW_BYTES)
+        q1, idx1 = W.decode_b1_inputs(dev, g1)
+        del x1
+        s1 = args.splits or _choose_num_kv_splits_mi355x(1, 1, W.TOPK, cu)
+        mla_b1 = lambda: triton_mla_sparse_attention(q1, kv1, idx1, W.SM_SCALE, num_kv_splits=args.splits)
+        graph1, _ = capture(torch, mla_b1, args.unroll)
+        for _ in range(Wm):
+            graph1.replay()
+        log("decode_b1")
+        us1 = timer.replay_loop(graph1, K // args.unroll) / args.unroll
+        g1_1, _ = capture(torch, mla_b1, 1)
+        us1_cold = timer.cold_loop(g1_1, min(K, 50), flush)
+        us1_single = timer.replay_loop(g1_1, min(K, 100))
+        del g1_1
+        bytes1 = W.mla_bytes(idx1, n_rows)
+        extra["decode_b1"] = {"us_per_step_warm": round(us1, 3), "us_per_step_cold": round(us1_cold, 3),
+                              "us_per_step_one_call_per_graph": round(us1_single, 3),
+                              "algorithmic_bytes": bytes1, "gbs_warm": round(bytes1 / (us1 * 1e-6) / 1e9, 1),
+                              "gbs_cold": round(bytes1 / (us1_cold * 1e-6) / 1e9, 1), "num_kv_splits": s1}
+        del graph1
+
+        # ------------------------------------------------------------ MoE align
+        moe = {}
+        gm = W.gen(dev, W.SEED_BENCH)
+        for b in (1, 2, 4, 8):
+            ids = W.moe_routes(b, dev, gm)
+            mg, _ = capture(torch, lambda ids=ids: titan_moe_align_small(ids), unroll=16)
+            for _ in range(5):
+                mg.replay()
+            samples = [timer.replay_loop(mg, 100) / 16 for _ in range(5)]
+            moe[f"B{b}"] = round(statistics.median(samples), 3)
+            del mg
+        extra["moe_align_us_per_call"] = moe
+        extra["moe_align_reference_us_per_call_sm80"] = {"B1": 1.63, "B2": 1.97, "B4": 1.97, "B8": 5.07}
+
+        # ------------------------------------------------------------ prefill-shaped
+        qp, idxp, new_rows, pslots = W.prefill_inputs(dev, g8)
+        pg, _ = capture(torch, lambda: triton_mla_sparse_attention(qp, kv8, idxp, W.SM_SCALE))
+        pg.replay()
+        log("prefill T=2048")
+        us_p = timer.replay_loop(pg, 5)
+        bytes_p = W.mla_bytes(idxp, n_rows)
+        flops_p = W.mla_flops(idxp, n_rows)
+        extra["prefill_t2048"] = {"us_per_call": round(us_p, 1), "algorithmic_bytes": bytes_p,
+                                  "gbs": round(bytes_p / (us_p * 1e-6) / 1e9, 1),
+                                  "tflops": round(flops_p / (us_p * 1e-6) / 1e12, 2)}
+        del pg
+        c5 = torch.zeros_like(cache8)
+        wpg, _ = capture(torch, lambda: store_int8(new_rows, c5, pslots))
+        us_ws = timer.replay_loop(wpg, 50)
+        extra["store_int8_2048_scattered"] = {"us_per_call": round(us_ws, 2),
+                                              "gbs": round(W.writer_bytes(2048) / (us_ws * 1e-6) / 1e9, 1)}
+        del wpg, c5
+
+        # ------------------------------------------------------------ CPU baseline
+        if not args.no_cpu:
+            import oracle
+            oracle.build()
+            rows8 = cache8.view(torch.uint8).cpu().numpy().reshape(-1, W.ROW_BYTES)
+            qn = q8.view(torch.int16).cpu().numpy().view(np.uint16)
+            ixn = idx8.cpu().numpy()
+            threads = oracle.default_threads()
+            log(f"CPU baseline on {threads} threads")
+            oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=threads)
+            t_cpu = []
+            for _ in range(5):
+                t0 = time.perf_counter()
+                oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=threads)
+                t_cpu.append(time.perf_counter() - t0)
+            us_cpu = statistics.median(t_cpu) * 1e6
+            t0 = time.perf_counter()
+            oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=1)
+            us_cpu1 = (time.perf_counter() - t0) * 1e6
+            cpu = {"value": round(bytes8 / (us_cpu * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads,
+                   "kind": "port",
+                   "sample": "the full decode_b8 workload (one B=8 sparse MLA step over the 262144-row cache), "
+                             "median of 5 runs of the C oracle",
+                   "us_per_step": round(us_cpu, 1), "us_per_step_1thread": round(us_cpu1, 1)}
+
+    # dominant kernel: sparse_mla_kernel (split attention); algorithmic bytes of
+    # the step over its event-timed average duration.  traffic: measured HBM-side
+    # bytes per dispatch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated).
+    ach = bytes8 / (us8_kernel * 1e-6) / 1e9
+    traffic = None
+    tf = ROOT / "profiles" / "hbm_bytes_per_dispatch.json"
+    if tf.exists() and args.splits in (None, s8):
+        d = json.loads(tf.read_text())["per_dispatch"].get(f"sparse_mla_kernel@{s8 * 8 * 512}")
+        if d:
+            traffic = d["fetch_bytes"] + d["write_bytes"]
+    roofline = {"bound": "hbm", "kernel": "sparse_mla_kernel", "achieved": round(ach, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                "traffic": traffic, "algorithmic_bytes": bytes8,
+                "avg_kernel_us": round(us8_kernel, 3)}
+    line = {
+        "metric": METRIC,
+        "value": round(gbs8, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": Wm,
+        "ms_per_step": round(us8 / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decode_b8: sparse NoPE MLA decode, B=8, 16 heads, 262144-row INT8 cache, "
+                               "2176 indices/query (locality-biased, 0-256 trailing pads), Student-t latents",
+                   "batch": 8, "context": n_rows, "topk": W.TOPK, "heads": 16, "num_kv_splits": s8,
+                   "timing": f"HIP graph replay, {args.unroll} steps per graph, warm"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "device": {"name": props.name, "cus": cu},
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

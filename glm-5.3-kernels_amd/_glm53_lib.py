@@ -18,6 +18,9 @@ EXPORTED = (
     "glm53_store_int8",
     "glm53_sparse_mla_workspace_bytes",
     "glm53_sparse_mla",
+    "glm53_sparse_mla_partials_bytes",
+    "glm53_sparse_mla_partials",
+    "glm53_sparse_mla_merge",
     "glm53_moe_align_small",
 )
 
@@ -46,6 +49,13 @@ def load():
     L.glm53_sparse_mla.restype = I
     L.glm53_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, I64, P, I64,
                                    P, I64, I64, P]
+    L.glm53_sparse_mla_partials_bytes.restype = I64
+    L.glm53_sparse_mla_partials_bytes.argtypes = [I64, I64, I64]
+    L.glm53_sparse_mla_partials.restype = I
+    L.glm53_sparse_mla_partials.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, I64, P,
+                                            I64, P]
+    L.glm53_sparse_mla_merge.restype = I
+    L.glm53_sparse_mla_merge.argtypes = [P, I64, I64, I64, I64, P, I64, I64, P]
     L.glm53_moe_align_small.restype = I
     L.glm53_moe_align_small.argtypes = [P, I, I64, P, P, P, P]
     version = L.glm53_abi_version()

@@ -21,6 +21,8 @@ SOURCES = ["store_int8.hip", "moe_align.hip", "sparse_mla.hip"]
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-ffp-contract=off",
+    # keep MFMA accumulators in VGPRs (no AGPR copies around VALU rescales)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]

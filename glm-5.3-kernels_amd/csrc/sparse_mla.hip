@@ -11,21 +11,25 @@
 // with one split the kernel writes bf16(acc / l) directly (:245-255).
 //
 // Work decomposition (one workgroup = one (split, token, 16-head group)):
-//   * 4 wavefronts; wavefront w owns latent columns [128w, 128w + 128).
-//   * Keys are processed in tiles of 32.  Lane (g = lane / 16, c = lane % 16)
-//     loads 32 bytes of the wave's slice from keys c and 16 + c, so every
-//     lane issues four independent 16-byte gathers per tile.
+//   * 8 wavefronts = 2 key groups x 4 latent slices.  Wave w owns latent
+//     columns [128 s, 128 s + 128) with s = w % 4, and the tiles of 32 keys of
+//     key group w / 4 (even / odd tiles), each key group running its own
+//     online softmax; the two are merged through LDS at the end.  Two waves
+//     per SIMD interleave their tiles, hiding each other's latencies.
+//   * Lane (g = lane / 16, c = lane % 16) gathers 32 bytes of its wave's
+//     slice from keys c and 16 + c of a tile: four 16-byte loads per tile.
+//     The gathers of a whole chunk (8 tiles, 256 keys) are issued before any
+//     is consumed, so a decode split pays one index and one row latency.
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 latents
-//     (the gathered int8 converted to bf16 in registers), B = Q^T, 4 K-steps
-//     per wave; the four partial S^T tiles of the waves are summed through
-//     LDS in a fixed order, so every wave holds the same full scores.
-//   * The C layout of S^T gives lane (g, c) head c and keys {4g+i, 16+4g+i};
-//     that is exactly the B operand P^T of O^T = V^T P^T, so the online
-//     softmax runs per lane without any shuffle of P.
+//     (int8 converted to bf16 in registers), B = Q^T, 4 K-steps per wave;
+//     the four slices' partial S^T are summed through LDS in a fixed order.
+//   * The C layout of S^T gives lane (g, c) head c and keys {4g+i, 16+4g+i}:
+//     exactly the B operand P^T of O^T = V^T P^T, so the softmax needs no
+//     shuffle of P; the per-head max and sum over the four 16-lane rows use
+//     v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip).
 //   * V^T comes from the same gathered rows: each wave stores its bf16 slice
-//     row-major in LDS and reads it back transposed with ds_read_b64_tr_b16
-//     (two reads per 16x32 operand).  O^T accumulates in 8 MFMA tiles
-//     (16 latents x 16 heads each) per wave.
+//     row-major in LDS and reads it back with ds_read_b64_tr_b16 (two reads
+//     per 16x32 operand).  O^T accumulates in 8 MFMA tiles per wave.
 #include "glm53_common.h"
 
 namespace glm53 {
@@ -34,9 +38,14 @@ namespace {
 constexpr int kLatent = 512;
 constexpr int kHeads = 16;       // heads per workgroup (one MFMA M/N tile)
 constexpr int kTile = 32;        // keys per tile
-constexpr int kWaves = 4;        // latent slices of 128
-constexpr int kSlice = kLatent / kWaves;
+constexpr int kSlices = 4;       // latent slices of 128
+constexpr int kGroups = 2;       // key groups
+constexpr int kWaves = kSlices * kGroups;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kSlice = kLatent / kSlices;
 constexpr int kVStride = kSlice + 16;  // bf16 per LDS row: 288 bytes, rows 8 banks apart
+constexpr int kChunkTiles = 8;         // tiles whose gathers are in flight together
+constexpr int kRounds = kChunkTiles / kGroups;
 constexpr float kNegLarge = -1.0e30f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -58,7 +67,32 @@ struct MlaArgs {
   int heads_padded;
   uint16_t* out;
   int64_t so_t, so_h;
+  int partials_only;   // write part/lse even for a single split
 };
+
+__device__ __forceinline__ float f4_get(const float4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// 2^x on the hardware exponential (v_exp_f32); results below 2^-126 flush to
+// 0, which only drops softmax weights smaller than 1e-38.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Max / sum of v over the four 16-lane rows at the same column, returned to
+// every lane in the same summation order: rows (0,1) and (2,3) are paired by
+// v_permlane16_swap, then the halves by v_permlane32_swap.
+__device__ __forceinline__ float rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // 16 int8 (one uint4) -> two bf16x8 (exact: |v| <= 128 fits bf16).
 __device__ __forceinline__ void i8x16_to_bf16(const uint4 v, bf16x8& lo, bf16x8& hi) {
@@ -81,14 +115,27 @@ __device__ __forceinline__ void i8x16_to_bf16(const uint4 v, bf16x8& lo, bf16x8&
   hi = __builtin_bit_cast(bf16x8, b);
 }
 
-__global__ __launch_bounds__(256) void sparse_mla_kernel(const MlaArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vbuf[kWaves][kTile][kVStride];
-  __shared__ float red[2][kWaves][8][64];
+struct __attribute__((aligned(16))) MlaShared {
+  union {
+    uint16_t vbuf[kWaves][kTile][kVStride];          // per-wave bf16 V slice of a tile
+    struct {
+      float acc[kSlices][32][64];                      // key group 1's accumulators
+      float ml[kHeads][2];                             // key group 1's (m, l) per head
+    } merge;
+  };
+  float red[2][kGroups][kSlices][64][8];               // partial S^T per slice
+  float scl[2][kChunkTiles][kTile];                    // row scales of the chunk
+};
+
+__global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
+  __shared__ MlaShared sh;
 
   const int split = blockIdx.x;
   const int t = blockIdx.y;
   const int hg = blockIdx.z;
   const int w = uniform(threadIdx.x >> 6);
+  const int sl = w & (kSlices - 1);
+  const int kg = w / kSlices;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   const int c = lane & 15;
@@ -99,14 +146,14 @@ __global__ __launch_bounds__(256) void sparse_mla_kernel(const MlaArgs a) {
   const int32_t* idx_t = a.idx + t * a.si_t;
 
   // Q^T fragment (B operand of S^T = K Q^T): head c, latents
-  // [128w + 32g, +32) -> four K-steps of 8.
+  // [128 sl + 32g, +32) -> four K-steps of 8.
   bf16x8 qf[4];
   {
     uint4 z = make_uint4(0, 0, 0, 0);
     uint4 q0 = z, q1 = z, q2 = z, q3 = z;
     if (head_ok) {
       const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + head * a.sq_h +
-                                                       kSlice * w + 32 * g);
+                                                       kSlice * sl + 32 * g);
       q0 = qp[0]; q1 = qp[1]; q2 = qp[2]; q3 = qp[3];
     }
     qf[0] = __builtin_bit_cast(bf16x8, q0);
@@ -120,180 +167,277 @@ __global__ __launch_bounds__(256) void sparse_mla_kernel(const MlaArgs a) {
   for (int i = 0; i < 8; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegLarge, l_run = 0.f;
 
-  int buf = 0;
-  for (int k0 = start; k0 < end; k0 += kTile, buf ^= 1) {
-    // Indices of the tile: lane l holds key (l & 31).
-    const int pos = k0 + (lane & 31);
-    int id = pos < end ? idx_t[pos] : -1;
-    if (id < 0 || static_cast<int64_t>(id) >= a.seq_kv) id = -1;
-
-    // Gather: keys c and 16 + c, bytes [128w + 32g, +32).
-    uint4 kd[2][2];
+  int buf = 0, cbuf = 0;
+  for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile, cbuf ^= 1) {
+    // ---- issue every load of the chunk: indices, then rows and scales.
+    // Round r of this key group is chunk tile 2r + kg.
+    int id[kRounds];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-      const int kid = __shfl(id, 16 * u + c, 64);
-      kd[u][0] = make_uint4(0, 0, 0, 0);
-      kd[u][1] = make_uint4(0, 0, 0, 0);
-      if (kid >= 0) {
-        const uint4* rp = reinterpret_cast<const uint4*>(a.kv + static_cast<int64_t>(kid) * a.skv +
-                                                         kSlice * w + 32 * g);
-        kd[u][0] = rp[0];
-        kd[u][1] = rp[1];
+    for (int r = 0; r < kRounds; r++) {
+      const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
+      int v = pos < end ? idx_t[pos] : -1;
+      if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv) v = -1;
+      id[r] = v;
+    }
+    uint4 kd[kRounds][2][2];
+    uint32_t vmask[kRounds];
+    float sv[kRounds];
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int kid = __shfl(id[r], 16 * u + c, 64);
+        kd[r][u][0] = make_uint4(0, 0, 0, 0);
+        kd[r][u][1] = make_uint4(0, 0, 0, 0);
+        if (kid >= 0) {
+          const uint4* rp = reinterpret_cast<const uint4*>(
+              a.kv + static_cast<int64_t>(kid) * a.skv + kSlice * sl + 32 * g);
+          kd[r][u][0] = rp[0];
+          kd[r][u][1] = rp[1];
+        }
       }
+      sv[r] = 0.f;
+      if (sl == 0 && lane < kTile && id[r] >= 0)
+        sv[r] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(id[r]) * a.skv + kLatent);
+      vmask[r] = static_cast<uint32_t>(__ballot(id[r] >= 0));
     }
-    // Scales of the keys this lane scores: 16u + 4g + i.
-    float sc[8];
-    int kvalid = 0;
+    if (sl == 0 && lane < kTile) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const int key = 16 * (j >> 2) + 4 * g + (j & 3);
-      const int kid = __shfl(id, key, 64);
-      sc[j] = 0.f;
-      if (kid >= 0) {
-        sc[j] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(kid) * a.skv + kLatent);
-        kvalid |= 1 << j;
+      for (int r = 0; r < kRounds; r++) sh.scl[cbuf][2 * r + kg][lane] = sv[r];
+    }
+
+    // ---- consume the chunk: one tile per key group per round.
+#pragma unroll
+    for (int r = 0; r < kRounds; r++, buf ^= 1) {
+      if (c0 + 2 * r * kTile >= end) break;                      // uniform across the workgroup
+      const bool has_tile = c0 + (2 * r + kg) * kTile < end;     // uniform across the wave
+
+      if (has_tile) {
+        f32x4 s_part[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          bf16x8 k01, k23, k45, k67;
+          i8x16_to_bf16(kd[r][u][0], k01, k23);
+          i8x16_to_bf16(kd[r][u][1], k45, k67);
+          f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k01, qf[0], sacc, 0, 0, 0);
+          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k23, qf[1], sacc, 0, 0, 0);
+          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k45, qf[2], sacc, 0, 0, 0);
+          sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k67, qf[3], sacc, 0, 0, 0);
+          s_part[u] = sacc;
+          // V slice for the PV product: row 16u + c, latents [32g, +32) of the slice.
+          uint4* vp = reinterpret_cast<uint4*>(&sh.vbuf[w][16 * u + c][32 * g]);
+          vp[0] = __builtin_bit_cast(uint4, k01);
+          vp[1] = __builtin_bit_cast(uint4, k23);
+          vp[2] = __builtin_bit_cast(uint4, k45);
+          vp[3] = __builtin_bit_cast(uint4, k67);
+        }
+        float4* rp = reinterpret_cast<float4*>(&sh.red[buf][kg][sl][lane][0]);
+        rp[0] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
+        rp[1] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
       }
-    }
+      __syncthreads();
+      if (!has_tile) continue;
 
-    // bf16 K fragments; partial S^T over this wave's slice.
-    f32x4 s_part[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-      bf16x8 k01, k23, k45, k67;
-      i8x16_to_bf16(kd[u][0], k01, k23);
-      i8x16_to_bf16(kd[u][1], k45, k67);
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k01, qf[0], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k23, qf[1], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k45, qf[2], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k67, qf[3], s, 0, 0, 0);
-      s_part[u] = s;
-      // V slice for the PV product: row 16u + c, latents [32g, +32) of the slice.
-      uint4* vp = reinterpret_cast<uint4*>(&vbuf[w][16 * u + c][32 * g]);
-      vp[0] = __builtin_bit_cast(uint4, k01);
-      vp[1] = __builtin_bit_cast(uint4, k23);
-      vp[2] = __builtin_bit_cast(uint4, k45);
-      vp[3] = __builtin_bit_cast(uint4, k67);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      red[buf][w][i][lane] = s_part[0][i];
-      red[buf][w][4 + i][lane] = s_part[1][i];
-    }
-    __syncthreads();
+      const int tile = 2 * r + kg;
+      const float4 sc0 = *reinterpret_cast<const float4*>(&sh.scl[cbuf][tile][4 * g]);
+      const float4 sc1 = *reinterpret_cast<const float4*>(&sh.scl[cbuf][tile][16 + 4 * g]);
+      const float sc[8] = {sc0.x, sc0.y, sc0.z, sc0.w, sc1.x, sc1.y, sc1.z, sc1.w};
+      const uint32_t kv_ok = ((vmask[r] >> (4 * g)) & 0xfu) | (((vmask[r] >> (16 + 4 * g)) & 0xfu) << 4);
 
-    // Full scores (fixed summation order over the four slices).
-    float s[8];
+      // Full scores (fixed summation order over the four slices).
+      float s[8];
+      {
+        float4 rr[kSlices][2];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      float v = red[buf][0][j][lane];
-      v += red[buf][1][j][lane];
-      v += red[buf][2][j][lane];
-      v += red[buf][3][j][lane];
-      v *= sc[j];
-      v *= a.scale_log2;
-      s[j] = (kvalid >> j) & 1 ? v : kNegLarge;
-    }
-    float mx = s[0];
+        for (int ss = 0; ss < kSlices; ss++) {
+          const float4* rp = reinterpret_cast<const float4*>(&sh.red[buf][kg][ss][lane][0]);
+          rr[ss][0] = rp[0];
+          rr[ss][1] = rp[1];
+        }
 #pragma unroll
-    for (int j = 1; j < 8; j++) mx = fmaxf(mx, s[j]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
-    float p[8];
-    float psum = 0.f;
+        for (int j = 0; j < 8; j++) {
+          float v = f4_get(rr[0][j >> 2], j & 3);
+          v += f4_get(rr[1][j >> 2], j & 3);
+          v += f4_get(rr[2][j >> 2], j & 3);
+          v += f4_get(rr[3][j >> 2], j & 3);
+          v *= sc[j];
+          v *= a.scale_log2;
+          s[j] = (kv_ok >> j) & 1 ? v : kNegLarge;
+        }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+      mx = rows_max(mx);
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      float pr[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      p[j] = (kvalid >> j) & 1 ? exp2f(s[j] - m_new) : 0.f;
-      psum += p[j];
-    }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+      for (int j = 0; j < 8; j++) pr[j] = (kv_ok >> j) & 1 ? fast_exp2(s[j] - m_new) : 0.f;
+      float psum = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+      psum = rows_sum(psum);
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
 
-    // P^T operand: k-slot 8g + j <-> key 16(j/4) + 4g + (j%4).
-    uint4 pw = make_uint4(pack_bf16x2(p[0] * sc[0], p[1] * sc[1]), pack_bf16x2(p[2] * sc[2], p[3] * sc[3]),
-                          pack_bf16x2(p[4] * sc[4], p[5] * sc[5]), pack_bf16x2(p[6] * sc[6], p[7] * sc[7]));
-    const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+      // P^T operand: k-slot 8g + j <-> key 16(j/4) + 4g + (j%4).
+      const uint4 pw = make_uint4(pack_bf16x2(pr[0] * sc[0], pr[1] * sc[1]),
+                                  pack_bf16x2(pr[2] * sc[2], pr[3] * sc[3]),
+                                  pack_bf16x2(pr[4] * sc[4], pr[5] * sc[5]),
+                                  pack_bf16x2(pr[6] * sc[6], pr[7] * sc[7]));
+      const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
 
-    // O^T += V^T P^T for the 8 latent tiles of this wave.
-    // ds_read_b64_tr_b16: in each 16-lane group, lane 4r + q addresses row r,
-    // columns [4q, 4q + 4); lane c receives column c of the 4 rows.
-    const int tr_row = 4 * g + (c >> 2);
-    const int tr_col = 4 * (c & 3);
+      // The running max changes rarely after the first tiles: rescale only
+      // when it moved for some head of this wave (alpha == 1 otherwise).
+      if (__ballot(alpha != 1.f)) {
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-      const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          GLM53_LDS(i16x4, &vbuf[w][tr_row][16 * dt + tr_col]));
-      const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          GLM53_LDS(i16x4, &vbuf[w][16 + tr_row][16 * dt + tr_col]));
-      const i32x2 v0i = __builtin_bit_cast(i32x2, v0);
-      const i32x2 v1i = __builtin_bit_cast(i32x2, v1);
-      const uint4 vv = make_uint4(v0i[0], v0i[1], v1i[0], v1i[1]);
-      f32x4 o = acc[dt];
-      o[0] *= alpha; o[1] *= alpha; o[2] *= alpha; o[3] *= alpha;
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, o, 0, 0, 0);
+        for (int dt = 0; dt < 8; dt++) {
+          acc[dt][0] *= alpha; acc[dt][1] *= alpha; acc[dt][2] *= alpha; acc[dt][3] *= alpha;
+        }
+      }
+      // O^T += V^T P^T for the 8 latent tiles of this wave.
+      // ds_read_b64_tr_b16: in each 16-lane group, lane 4r + q addresses row r,
+      // columns [4q, 4q + 4); lane c receives column c of the 4 rows.
+      const int tr_row = 4 * g + (c >> 2);
+      const int tr_col = 4 * (c & 3);
+#pragma unroll
+      for (int dt = 0; dt < 8; dt++) {
+        const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            GLM53_LDS(i16x4, &sh.vbuf[w][tr_row][16 * dt + tr_col]));
+        const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            GLM53_LDS(i16x4, &sh.vbuf[w][16 + tr_row][16 * dt + tr_col]));
+        const i32x2 v0i = __builtin_bit_cast(i32x2, v0);
+        const i32x2 v1i = __builtin_bit_cast(i32x2, v1);
+        const uint4 vv = make_uint4(v0i[0], v0i[1], v1i[0], v1i[1]);
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, acc[dt], 0, 0, 0);
+      }
     }
   }
 
-  if (!head_ok) return;
-  const float l_safe = l_run > 0.f ? l_run : 1.f;
-  if (a.num_splits == 1) {
-    uint16_t* op = a.out + t * a.so_t + head * a.so_h + kSlice * w + 4 * g;
+  // ---- merge key group 1 into key group 0 (vbuf is free after the barrier).
+  __syncthreads();
+  if (kg == 1) {
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) sh.merge.acc[sl][4 * dt + i][lane] = acc[dt][i];
+    }
+    if (sl == 0 && g == 0) {
+      sh.merge.ml[c][0] = m_run;
+      sh.merge.ml[c][1] = l_run;
+    }
+  }
+  __syncthreads();
+  if (kg == 1 || !head_ok) return;
+  {
+    const float m1 = sh.merge.ml[c][0];
+    const float l1 = sh.merge.ml[c][1];
+    const float mm = fmaxf(m_run, m1);
+    const float a0 = fast_exp2(m_run - mm);
+    const float a1 = fast_exp2(m1 - mm);
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[dt][i] = acc[dt][i] * a0 + sh.merge.acc[sl][4 * dt + i][lane] * a1;
+    }
+    l_run = l_run * a0 + l1 * a1;
+    m_run = mm;
+  }
+
+  // 1 / l once, then multiplies (the reference divides; the two differ by at
+  // most one fp32 ulp before the bf16 / fp32 store).
+  const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
+  if (a.num_splits == 1 && !a.partials_only) {
+    uint16_t* op = a.out + t * a.so_t + head * a.so_h + kSlice * sl + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) {
       uint2 o;
-      o.x = pack_bf16x2(acc[dt][0] / l_safe, acc[dt][1] / l_safe);
-      o.y = pack_bf16x2(acc[dt][2] / l_safe, acc[dt][3] / l_safe);
+      o.x = pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l);
+      o.y = pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l);
       *reinterpret_cast<uint2*>(op + 16 * dt) = o;
     }
   } else {
     const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
-    float* pp = a.part + row * kLatent + kSlice * w + 4 * g;
+    float* pp = a.part + row * kLatent + kSlice * sl + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) {
-      float4 o = make_float4(acc[dt][0] / l_safe, acc[dt][1] / l_safe, acc[dt][2] / l_safe,
-                             acc[dt][3] / l_safe);
+      float4 o = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l, acc[dt][2] * inv_l,
+                             acc[dt][3] * inv_l);
       *reinterpret_cast<float4*>(pp + 16 * dt) = o;
     }
-    if (w == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
+    if (sl == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
   }
 }
 
-// N-way LSE merge (kernels/titan_mla.py:403-429): one workgroup per (t, h),
-// 128 threads x 4 latents.
-__global__ __launch_bounds__(128) void sparse_mla_merge_kernel(const float* __restrict__ part,
+// N-way LSE merge (kernels/titan_mla.py:403-429).  One workgroup per
+// (token, head, 128-latent quarter); 256 threads = 8 split lanes x 32 chunks
+// of 4 latents.  All split LSEs are loaded at once and their maximum M taken
+// first; then out = sum_s e^{lse_s - M} part_s / sum_s e^{lse_s - M}, which is
+// the reference's running rescaled sum written without a serial dependency.
+// Split lanes are summed in a fixed order, so the result is deterministic.
+// Empty splits carry lse = -inf and weigh 0; no valid split gives 0.
+constexpr int kMergeLanes = 8;
+constexpr int kMaxMergeSplits = 1024;
+
+__global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __restrict__ part,
                                                                const float* __restrict__ lse,
                                                                int num_splits, int heads_padded,
                                                                int num_heads,
                                                                uint16_t* __restrict__ out,
                                                                int64_t so_t, int64_t so_h) {
+  __shared__ float wts[kMaxMergeSplits];
+  __shared__ float red_m[256 / 64];
+  __shared__ __attribute__((aligned(16))) float4 part_sum[kMergeLanes][32];
   const int t = blockIdx.x / num_heads;
   const int h = blockIdx.x % num_heads;
-  const int d = threadIdx.x * 4;
-  float e_max = kNegLarge, e_sum = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s = 0; s < num_splits; s++) {
-    const int64_t row = (static_cast<int64_t>(t) * num_splits + s) * heads_padded + h;
-    const float tl = lse[row];
-    const float4 v = *reinterpret_cast<const float4*>(part + row * kLatent + d);
-    const float n_max = fmaxf(tl, e_max);
-    const float old_scale = expf(e_max - n_max);
-    const float e = expf(tl - n_max);
-    acc.x = acc.x * old_scale + e * v.x;
-    acc.y = acc.y * old_scale + e * v.y;
-    acc.z = acc.z * old_scale + e * v.z;
-    acc.w = acc.w * old_scale + e * v.w;
-    e_sum = e_sum * old_scale + e;
-    e_max = n_max;
+  const int quarter = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int sl = tid >> 5;          // split lane
+  const int ch = tid & 31;          // 4-latent chunk in the quarter
+  const int64_t row0 = static_cast<int64_t>(t) * num_splits * heads_padded + h;
+
+  // LSEs -> LDS, block max.
+  float m = kNegLarge;
+  for (int s = tid; s < num_splits; s += 256) {
+    const float v = lse[row0 + static_cast<int64_t>(s) * heads_padded];
+    wts[s] = v;
+    m = fmaxf(m, v);
   }
-  const float es = e_sum > 0.f ? e_sum : 1.f;
-  uint2 o;
-  o.x = pack_bf16x2(acc.x / es, acc.y / es);
-  o.y = pack_bf16x2(acc.z / es, acc.w / es);
-  *reinterpret_cast<uint2*>(out + t * so_t + h * so_h + d) = o;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  if ((tid & 63) == 0) red_m[tid >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  for (int s = tid; s < num_splits; s += 256) wts[s] = expf(wts[s] - m);
+  __syncthreads();
+
+  float den = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int d = quarter * 128 + ch * 4;
+#pragma unroll 4
+  for (int s = sl; s < num_splits; s += kMergeLanes) {
+    const float e = wts[s];
+    const float4 v = *reinterpret_cast<const float4*>(
+        part + (row0 + static_cast<int64_t>(s) * heads_padded) * kLatent + d);
+    acc.x += e * v.x;
+    acc.y += e * v.y;
+    acc.z += e * v.z;
+    acc.w += e * v.w;
+  }
+  part_sum[sl][ch] = acc;
+  for (int s = 0; s < num_splits; s++) den += wts[s];
+  __syncthreads();
+  if (sl == 0) {
+    float4 r = part_sum[0][ch];
+#pragma unroll
+    for (int k = 1; k < kMergeLanes; k++) {
+      const float4 v = part_sum[k][ch];
+      r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
+    }
+    const float inv = 1.f / (den > 0.f ? den : 1.f);
+    uint2 o;
+    o.x = pack_bf16x2(r.x * inv, r.y * inv);
+    o.y = pack_bf16x2(r.z * inv, r.w * inv);
+    *reinterpret_cast<uint2*>(out + t * so_t + h * so_h + d) = o;
+  }
 }
 
 }  // namespace
@@ -301,36 +445,27 @@ __global__ __launch_bounds__(128) void sparse_mla_merge_kernel(const float* __re
 
 using namespace glm53;
 
-extern "C" int64_t glm53_sparse_mla_workspace_bytes(int64_t num_tokens, int64_t num_heads,
-                                                    int64_t num_splits) {
-  if (num_tokens < 0 || num_heads < 1 || num_splits < 1) return -1;
-  if (num_splits == 1) return 0;
-  const int64_t hp = (num_heads + kHeads - 1) / kHeads * kHeads;
-  const int64_t rows = num_tokens * num_splits * hp;
-  return rows * kLatent * 4 + rows * 4;
+namespace glm53 {
+namespace {
+
+int64_t partial_rows(int64_t num_tokens, int64_t num_heads, int64_t num_splits) {
+  return num_tokens * num_splits * ((num_heads + kHeads - 1) / kHeads * kHeads);
 }
 
-extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
-                                int64_t skv_t, int64_t seq_kv, const int32_t* indices,
-                                int64_t si_t, int64_t num_tokens, int64_t num_heads, int64_t topk,
-                                double sm_scale, int64_t num_splits, void* workspace,
-                                int64_t workspace_bytes, void* out, int64_t so_t, int64_t so_h,
-                                void* stream) {
+// Validates the attention arguments and fills MlaArgs (all but the outputs).
+int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* kv, int64_t skv_t,
+            int64_t seq_kv, const int32_t* indices, int64_t si_t, int64_t num_tokens,
+            int64_t num_heads, int64_t topk, double sm_scale, int64_t num_splits) {
   if (num_tokens < 0 || num_heads < 1 || topk < 0 || num_splits < 1 || seq_kv < 0)
     return GLM53_ERR_BAD_SHAPE;
-  if (num_tokens == 0) return 0;
-  if (!q || !out || (!kv && seq_kv > 0) || (!indices && topk > 0)) return GLM53_ERR_NULL_POINTER;
-  if (topk > 0x7fffffff || num_tokens > 0x7fffffff || num_splits > 65535 ||
+  if (num_tokens > 0 && (!q || (!kv && seq_kv > 0) || (!indices && topk > 0)))
+    return GLM53_ERR_NULL_POINTER;
+  if (topk > 0x7fffffff || num_tokens > 0x7fffffff || num_splits > kMaxMergeSplits ||
       (num_heads + kHeads - 1) / kHeads > 65535)
     return GLM53_ERR_BAD_SHAPE;
   if (reinterpret_cast<uintptr_t>(q) % 16 || sq_t % 8 || sq_h % 8 ||
-      reinterpret_cast<uintptr_t>(kv) % 16 || skv_t % 16 || reinterpret_cast<uintptr_t>(out) % 8 ||
-      so_t % 4 || so_h % 4)
+      reinterpret_cast<uintptr_t>(kv) % 16 || skv_t % 16)
     return GLM53_ERR_MISALIGNED;
-  const int64_t need = glm53_sparse_mla_workspace_bytes(num_tokens, num_heads, num_splits);
-  if (num_splits > 1 && (!workspace || workspace_bytes < need)) return GLM53_ERR_WORKSPACE;
-
-  MlaArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.sq_t = sq_t;
   a.sq_h = sq_h;
@@ -345,23 +480,115 @@ extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const
   a.split_len = static_cast<int>((topk + num_splits - 1) / num_splits);
   a.scale_log2 = static_cast<float>(sm_scale * 1.4426950408889634);
   a.heads_padded = static_cast<int>((num_heads + kHeads - 1) / kHeads * kHeads);
-  const int64_t rows = num_tokens * num_splits * a.heads_padded;
+  a.part = nullptr;
+  a.lse = nullptr;
+  a.out = nullptr;
+  a.partials_only = 0;
+  a.so_t = a.so_h = 0;
+  return 0;
+}
+
+void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
+                  static_cast<unsigned>(a.heads_padded / kHeads));
+  hipLaunchKernelGGL(sparse_mla_kernel, grid, dim3(kThreads), 0, st, a);
+}
+
+void launch_merge(const float* part, const float* lse, int64_t num_tokens, int num_splits,
+                  int heads_padded, int num_heads, uint16_t* out, int64_t so_t, int64_t so_h,
+                  hipStream_t st) {
+  hipLaunchKernelGGL(sparse_mla_merge_kernel, dim3(static_cast<unsigned>(num_tokens * num_heads), 4),
+                     dim3(256), 0, st, part, lse, num_splits, heads_padded, num_heads, out, so_t, so_h);
+}
+
+}  // namespace
+}  // namespace glm53
+
+extern "C" int64_t glm53_sparse_mla_workspace_bytes(int64_t num_tokens, int64_t num_heads,
+                                                    int64_t num_splits) {
+  if (num_tokens < 0 || num_heads < 1 || num_splits < 1) return -1;
+  if (num_splits == 1) return 0;
+  return glm53_sparse_mla_partials_bytes(num_tokens, num_heads, num_splits);
+}
+
+extern "C" int64_t glm53_sparse_mla_partials_bytes(int64_t num_tokens, int64_t num_heads,
+                                                   int64_t num_splits) {
+  if (num_tokens < 0 || num_heads < 1 || num_splits < 1) return -1;
+  const int64_t rows = partial_rows(num_tokens, num_heads, num_splits);
+  return rows * kLatent * 4 + rows * 4;
+}
+
+extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
+                                int64_t skv_t, int64_t seq_kv, const int32_t* indices,
+                                int64_t si_t, int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                double sm_scale, int64_t num_splits, void* workspace,
+                                int64_t workspace_bytes, void* out, int64_t so_t, int64_t so_h,
+                                void* stream) {
+  MlaArgs a;
+  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, indices, si_t, num_tokens, num_heads, topk,
+                   sm_scale, num_splits);
+  if (rc) return rc;
+  if (num_tokens == 0) return 0;
+  if (!out) return GLM53_ERR_NULL_POINTER;
+  if (reinterpret_cast<uintptr_t>(out) % 8 || so_t % 4 || so_h % 4) return GLM53_ERR_MISALIGNED;
+  const int64_t need = glm53_sparse_mla_workspace_bytes(num_tokens, num_heads, num_splits);
+  if (num_splits > 1 && (!workspace || workspace_bytes < need)) return GLM53_ERR_WORKSPACE;
+  const int64_t rows = partial_rows(num_tokens, num_heads, num_splits);
   a.part = num_splits > 1 ? static_cast<float*>(workspace) : nullptr;
   a.lse = num_splits > 1 ? static_cast<float*>(workspace) + rows * kLatent : nullptr;
   a.out = static_cast<uint16_t*>(out);
   a.so_t = so_t;
   a.so_h = so_h;
-
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
-  const dim3 grid(static_cast<unsigned>(num_splits), static_cast<unsigned>(num_tokens),
-                  static_cast<unsigned>(a.heads_padded / kHeads));
-  hipLaunchKernelGGL(sparse_mla_kernel, grid, dim3(256), 0, st, a);
-  if (num_splits > 1) {
-    hipLaunchKernelGGL(sparse_mla_merge_kernel, dim3(static_cast<unsigned>(num_tokens * num_heads)),
-                       dim3(128), 0, st, a.part, a.lse, a.num_splits, a.heads_padded, a.num_heads,
-                       a.out, so_t, so_h);
-  }
+  launch_attention(a, num_tokens, st);
+  if (num_splits > 1)
+    launch_merge(a.part, a.lse, num_tokens, a.num_splits, a.heads_padded, a.num_heads, a.out, so_t,
+                 so_h, st);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int glm53_sparse_mla_partials(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
+                                         int64_t skv_t, int64_t seq_kv, const int32_t* indices,
+                                         int64_t si_t, int64_t num_tokens, int64_t num_heads,
+                                         int64_t topk, double sm_scale, int64_t num_splits,
+                                         void* partials, int64_t partials_bytes, void* stream) {
+  MlaArgs a;
+  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, indices, si_t, num_tokens, num_heads, topk,
+                   sm_scale, num_splits);
+  if (rc) return rc;
+  if (num_tokens == 0) return 0;
+  const int64_t need = glm53_sparse_mla_partials_bytes(num_tokens, num_heads, num_splits);
+  if (!partials || partials_bytes < need) return GLM53_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(partials) % 16) return GLM53_ERR_MISALIGNED;
+  const int64_t rows = partial_rows(num_tokens, num_heads, num_splits);
+  a.part = static_cast<float*>(partials);
+  a.lse = static_cast<float*>(partials) + rows * kLatent;
+  a.partials_only = 1;
+  (void)hipGetLastError();
+  launch_attention(a, num_tokens, static_cast<hipStream_t>(stream));
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int glm53_sparse_mla_merge(const void* partials, int64_t partials_bytes, int64_t num_tokens,
+                                      int64_t num_heads, int64_t num_splits, void* out, int64_t so_t,
+                                      int64_t so_h, void* stream) {
+  if (num_tokens < 0 || num_heads < 1 || num_splits < 1 || num_splits > kMaxMergeSplits)
+    return GLM53_ERR_BAD_SHAPE;
+  if (num_tokens == 0) return 0;
+  const int64_t need = glm53_sparse_mla_partials_bytes(num_tokens, num_heads, num_splits);
+  if (!partials || partials_bytes < need) return GLM53_ERR_WORKSPACE;
+  if (!out) return GLM53_ERR_NULL_POINTER;
+  if (reinterpret_cast<uintptr_t>(partials) % 16 || reinterpret_cast<uintptr_t>(out) % 8 || so_t % 4 ||
+      so_h % 4)
+    return GLM53_ERR_MISALIGNED;
+  const int64_t rows = partial_rows(num_tokens, num_heads, num_splits);
+  const int hp = static_cast<int>((num_heads + kHeads - 1) / kHeads * kHeads);
+  const float* part = static_cast<const float*>(partials);
+  (void)hipGetLastError();
+  launch_merge(part, part + rows * kLatent, num_tokens, static_cast<int>(num_splits), hp,
+               static_cast<int>(num_heads), static_cast<uint16_t*>(out), so_t, so_h,
+               static_cast<hipStream_t>(stream));
   return static_cast<int>(hipGetLastError());
 }
 

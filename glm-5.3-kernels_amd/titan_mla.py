@@ -62,6 +62,31 @@ def _choose_num_kv_splits(num_tokens: int, num_head_groups: int, index_topk: int
     return max(1, num_kv_splits)
 
 
+@functools.lru_cache(maxsize=256)
+def _choose_num_kv_splits_mi355x(num_tokens: int, num_head_groups: int, index_topk: int,
+                                 cu_count: int) -> int:
+    """Split count used when the caller leaves num_kv_splits to the library.
+
+    The split kernel runs one 512-thread workgroup per (split, token, head
+    group) and needs ~106 KB of LDS, so one workgroup fits a compute unit.
+    Decode latency is set by the per-workgroup chain (index load -> row
+    gather -> tiles), so the top-k axis is cut into as many whole 32-key
+    tiles per split as still lets every workgroup start in the first wave:
+    the largest divisor of topk / 32 with tokens * groups * splits <= CUs.
+    (The reference's _choose_num_kv_splits targets Triton on 70 SMs and is
+    kept above, unchanged, for callers that want its exact answers.)
+    """
+    base = num_tokens * num_head_groups
+    if base == 0 or index_topk % _MIN_BLOCK_N:
+        return 1
+    tiles = index_topk // _MIN_BLOCK_N
+    best = 1
+    for d in range(1, tiles + 1):
+        if tiles % d == 0 and base * d <= cu_count:
+            best = d
+    return best
+
+
 def triton_mla_sparse_attention(
     q: torch.Tensor,
     kv: torch.Tensor,
@@ -79,7 +104,8 @@ def triton_mla_sparse_attention(
                    are masked
         sm_scale:  softmax scale
         num_kv_splits: None/0 = heuristic, 1 = single pass, n = n splits
-        sm_count:  compute-unit count for the heuristic (queried if None)
+        sm_count:  compute-unit count for the heuristic (queried if None);
+                   the split policy is _choose_num_kv_splits_mi355x
 
     Returns:
         out: [num_tokens, num_heads_q, 512] bf16
@@ -104,7 +130,7 @@ def triton_mla_sparse_attention(
     if num_kv_splits is None or num_kv_splits == 0:
         if sm_count is None:
             sm_count = num_compute_units(q.device.index)
-        num_kv_splits = _choose_num_kv_splits(num_tokens, num_head_groups, index_topk, sm_count)
+        num_kv_splits = _choose_num_kv_splits_mi355x(num_tokens, num_head_groups, index_topk, sm_count)
     if num_kv_splits < 1:
         raise ValueError(f"num_kv_splits must be >= 1, got {num_kv_splits}")
 
@@ -135,6 +161,41 @@ def triton_mla_sparse_attention(
             out.data_ptr(), out.stride(0), out.stride(1),
             _lib.stream_handle(q.device))
     _lib.check(rc, "glm53_sparse_mla")
+    return out
+
+
+def sparse_mla_partials(q, kv, indices, sm_scale, num_kv_splits):
+    """First stage only: per-split normalised outputs and LSEs (fp32) in one
+    buffer laid out as glm53.h documents (part [T*S*Hp, 512] then lse
+    [T*S*Hp], Hp = heads rounded up to 16).  For callers that merge splits
+    themselves, e.g. after gathering one token's splits from several devices."""
+    assert q.dim() == 3 and q.shape[2] == _BLOCK_DMODEL and q.dtype == torch.bfloat16
+    assert kv.dtype == torch.int8 and kv.shape[1] == 1 and kv.shape[2] == _ROW_BYTES
+    assert indices.dtype == torch.int32 and indices.stride(2) == 1
+    if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    T, H, _ = q.shape
+    L = _lib.load()
+    nbytes = L.glm53_sparse_mla_partials_bytes(T, H, num_kv_splits)
+    buf = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = L.glm53_sparse_mla_partials(q.data_ptr(), q.stride(0), q.stride(1), kv.data_ptr(), kv.stride(0),
+                                         kv.shape[0], indices.data_ptr(), indices.stride(0), T, H,
+                                         indices.shape[2], float(sm_scale), num_kv_splits, buf.data_ptr(),
+                                         nbytes, _lib.stream_handle(q.device))
+    _lib.check(rc, "glm53_sparse_mla_partials")
+    return buf
+
+
+def sparse_mla_merge(partials, num_tokens, num_heads, num_kv_splits):
+    """Second stage: log-sum-exp merge of sparse_mla_partials' buffer."""
+    out = torch.empty((num_tokens, num_heads, _BLOCK_DV), dtype=torch.bfloat16, device=partials.device)
+    L = _lib.load()
+    with torch.cuda.device(partials.device):
+        rc = L.glm53_sparse_mla_merge(partials.data_ptr(), partials.numel(), num_tokens, num_heads,
+                                      num_kv_splits, out.data_ptr(), out.stride(0), out.stride(1),
+                                      _lib.stream_handle(partials.device))
+    _lib.check(rc, "glm53_sparse_mla_merge")
     return out
 
 

@@ -68,7 +68,7 @@ int glm53_store_int8(const void* x, int64_t x_row_stride,
  *            index outside [0, seq_kv) is masked out.
  *   sm_scale softmax scale; logits are q.k * scale_j * fp32(sm_scale*log2 e)
  *            in base 2, as the reference computes them.
- *   num_splits  >= 1; the top-k axis is cut into num_splits slices of
+ *   num_splits  1..1024; the top-k axis is cut into num_splits slices of
  *            ceil(topk / num_splits) indices whose partial results are merged
  *            by log-sum-exp.  1 = single pass.
  *   workspace   device scratch of glm53_sparse_mla_workspace_bytes(...)
@@ -86,6 +86,35 @@ int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h,
                      void* workspace, int64_t workspace_bytes,
                      void* out, int64_t so_t, int64_t so_h,
                      void* stream);
+
+/*
+ * The two stages of glm53_sparse_mla, exposed for callers that merge split
+ * results themselves (for example after gathering one token's splits from
+ * several devices).  Same stages as the reference's _sparse_mla_kernel_split
+ * and _sparse_mla_merge_kernel (kernels/titan_mla.py:258-429).
+ *
+ * Partials layout (fp32), rows = num_tokens * num_splits * Hp with
+ * Hp = num_heads rounded up to a multiple of 16, row r = (t * num_splits +
+ * s) * Hp + h:
+ *   part[rows][512]  normalised split output acc / l  (0 for an empty split)
+ *   lse[rows]        (m + log2 l) * ln 2, natural-log LSE (-inf when empty)
+ * glm53_sparse_mla_partials writes them for any num_splits >= 1;
+ * glm53_sparse_mla_merge combines them into bf16 out with log-sum-exp
+ * weights.  glm53_sparse_mla_partials_bytes gives the buffer size.
+ */
+int64_t glm53_sparse_mla_partials_bytes(int64_t num_tokens, int64_t num_heads,
+                                        int64_t num_splits);
+int glm53_sparse_mla_partials(const void* q, int64_t sq_t, int64_t sq_h,
+                              const void* kv, int64_t skv_t, int64_t seq_kv,
+                              const int32_t* indices, int64_t si_t,
+                              int64_t num_tokens, int64_t num_heads, int64_t topk,
+                              double sm_scale, int64_t num_splits,
+                              void* partials, int64_t partials_bytes,
+                              void* stream);
+int glm53_sparse_mla_merge(const void* partials, int64_t partials_bytes,
+                           int64_t num_tokens, int64_t num_heads,
+                           int64_t num_splits, void* out, int64_t so_t,
+                           int64_t so_h, void* stream);
 
 /*
  * Stable MoE route alignment for 1..8 tokens, top-8 routing, 288 experts,

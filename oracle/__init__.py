@@ -43,7 +43,8 @@ _lib = None
 
 def build(force: bool = False) -> Path:
     """Compile liboracle.so with the committed Makefile."""
-    if force or not LIB_PATH.exists():
+    src = HERE / "glm53_oracle.c"
+    if force or not LIB_PATH.exists() or LIB_PATH.stat().st_mtime < src.stat().st_mtime:
         subprocess.run(["make", "-s", "-C", str(HERE)] + (["-B"] if force else []), check=True)
     return LIB_PATH
 
@@ -60,12 +61,12 @@ def lib():
         L.oracle_quantize_row.argtypes = [P, P]
         L.oracle_moe_align.argtypes = [P, I64, P, P, P]
         L.oracle_moe_align_pairwise.argtypes = [P, I64, P, P, P]
-        L.oracle_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, F, I64, I64, P, I64, I64, I]
+        L.oracle_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, F, I64, I64, I64, P, I64, I64, I]
         L.oracle_sparse_mla.restype = None
         L.oracle_sparse_mla_f64.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, P, I]
         L.oracle_sparse_mla_f64.restype = None
         L.oracle_abi_version.restype = I
-        assert L.oracle_abi_version() == 1
+        assert L.oracle_abi_version() == 2
         _lib = L
     return _lib
 
@@ -179,8 +180,10 @@ def _mla_args(q_u16, rows, idx):
 
 
 def sparse_mla(q_u16: np.ndarray, rows: np.ndarray, idx: np.ndarray, sm_scale: float,
-               n_splits: int = 1, block_n: int = 32, nthreads: int = 1) -> np.ndarray:
-    """Faithful restatement: returns bf16 bits [T, H, 512]."""
+               n_splits: int = 1, block_n: int = 32, nthreads: int = 1, groups: int = 1) -> np.ndarray:
+    """Faithful restatement: returns bf16 bits [T, H, 512].  groups > 1 deals
+    each split's tiles round-robin to that many online-softmax streams merged
+    at the end (the HIP kernel's key groups); groups = 1 is the reference."""
     q_u16, rows, idx = _mla_args(q_u16, rows, idx)
     T, H, _ = q_u16.shape
     topk = idx.shape[1]
@@ -188,7 +191,7 @@ def sparse_mla(q_u16: np.ndarray, rows: np.ndarray, idx: np.ndarray, sm_scale: f
     sm_scale_log2 = np.float32(sm_scale * LOG2E)
     lib().oracle_sparse_mla(_ptr(q_u16), q_u16.strides[0] // 2, q_u16.strides[1] // 2, _ptr(rows),
                             rows.strides[0], rows.shape[0], _ptr(idx), idx.strides[0] // 4, T, H, topk,
-                            float(sm_scale_log2), int(n_splits), int(block_n), _ptr(out),
+                            float(sm_scale_log2), int(n_splits), int(block_n), int(groups), _ptr(out),
                             out.strides[0] // 2, out.strides[1] // 2, nthreads)
     return out
 

@@ -163,17 +163,22 @@ void oracle_moe_align_pairwise(const int64_t* ids, int64_t R, int32_t* sorted,
 
 /* One head, one contiguous range [start, end) of the top-k axis, processed in
  * tiles of block_n keys exactly as _sparse_mla_compute_tile (:117-180).
- * acc (512 floats) / *m / *l receive the running accumulators. */
-static void mla_range(const uint16_t* qh, const uint8_t* kv, int64_t skv,
-                      int64_t seq_kv, const int32_t* idx, int64_t start,
-                      int64_t end, float sm_scale_log2, int64_t block_n,
-                      float* acc, float* m_out, float* l_out,
-                      float* qk, float* kscale, int32_t* kid) {
+ * acc (512 floats) / *m / *l receive the running accumulators.
+ * With groups > 1 the tiles are dealt round-robin (tile i -> stream i % groups)
+ * to independent online-softmax streams that are combined at the end in
+ * stream order with base-2 rescaling (m = max m_g, acc = sum acc_g 2^(m_g - m),
+ * l = sum l_g 2^(m_g - m)): the reduction structure of the HIP kernel's key
+ * groups.  groups = 1 is the reference's single stream. */
+static void mla_stream(const float* qf, const uint8_t* kv, int64_t skv,
+                       int64_t seq_kv, const int32_t* idx, int64_t start,
+                       int64_t end, float sm_scale_log2, int64_t block_n,
+                       int64_t groups, int64_t gsel, float* acc, float* m_out,
+                       float* l_out, float* qk, float* kscale, int32_t* kid) {
   float e_max = NEG_LARGE, e_sum = 0.0f;
   for (int d = 0; d < LATENT; d++) acc[d] = 0.0f;
-  float qf[LATENT];
-  for (int d = 0; d < LATENT; d++) qf[d] = bf16_to_f32(qh[d]);
-  for (int64_t s0 = start; s0 < end; s0 += block_n) {
+  int64_t tile = 0;
+  for (int64_t s0 = start; s0 < end; s0 += block_n, tile++) {
+    if (tile % groups != gsel) continue;
     float tile_max = NEG_LARGE;
     for (int64_t j = 0; j < block_n; j++) {
       int64_t pos = s0 + j;
@@ -212,17 +217,47 @@ static void mla_range(const uint16_t* qh, const uint8_t* kv, int64_t skv,
   *l_out = e_sum;
 }
 
+static void mla_range(const uint16_t* qh, const uint8_t* kv, int64_t skv,
+                      int64_t seq_kv, const int32_t* idx, int64_t start,
+                      int64_t end, float sm_scale_log2, int64_t block_n,
+                      int64_t groups, float* acc, float* m_out, float* l_out,
+                      float* qk, float* kscale, int32_t* kid) {
+  float qf[LATENT];
+  for (int d = 0; d < LATENT; d++) qf[d] = bf16_to_f32(qh[d]);
+  if (groups <= 1) {
+    mla_stream(qf, kv, skv, seq_kv, idx, start, end, sm_scale_log2, block_n, 1, 0, acc, m_out,
+               l_out, qk, kscale, kid);
+    return;
+  }
+  float gacc[LATENT];
+  float m = NEG_LARGE, l = 0.0f;
+  for (int d = 0; d < LATENT; d++) acc[d] = 0.0f;
+  for (int64_t gsel = 0; gsel < groups; gsel++) {
+    float mg, lg;
+    mla_stream(qf, kv, skv, seq_kv, idx, start, end, sm_scale_log2, block_n, groups, gsel, gacc,
+               &mg, &lg, qk, kscale, kid);
+    float mm = mg > m ? mg : m;
+    float a_old = exp2f(m - mm), a_new = exp2f(mg - mm);
+    for (int d = 0; d < LATENT; d++) acc[d] = acc[d] * a_old + gacc[d] * a_new;
+    l = l * a_old + lg * a_new;
+    m = mm;
+  }
+  *m_out = m;
+  *l_out = l;
+}
+
 /* q: bf16 [T, H, 512] with strides sq_t, sq_h (elements); kv: byte base of
  * rows with stride skv (bytes), seq_kv rows; idx: int32 [T, topk] with stride
  * si_t; out: bf16 [T, H, 512] with strides so_t, so_h.  n_splits >= 1 follows
  * the split-KV + merge path (:258-429) when > 1, the single pass (:185-255)
- * when 1.  block_n is the tile width of the online softmax. */
+ * when 1.  block_n is the tile width of the online softmax; groups > 1 deals
+ * the tiles of each split to that many streams (see mla_range). */
 void oracle_sparse_mla(const uint16_t* q, int64_t sq_t, int64_t sq_h,
                        const uint8_t* kv, int64_t skv, int64_t seq_kv,
                        const int32_t* idx, int64_t si_t, int64_t T, int64_t H,
                        int64_t topk, float sm_scale_log2, int64_t n_splits,
-                       int64_t block_n, uint16_t* out, int64_t so_t,
-                       int64_t so_h, int nthreads) {
+                       int64_t block_n, int64_t groups, uint16_t* out,
+                       int64_t so_t, int64_t so_h, int nthreads) {
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
 #pragma omp parallel for collapse(2) schedule(dynamic) if (nthreads != 1)
@@ -238,7 +273,7 @@ void oracle_sparse_mla(const uint16_t* q, int64_t sq_t, int64_t sq_h,
       uint16_t* oh = out + t * so_t + h * so_h;
       if (n_splits <= 1) {
         float m, l;
-        mla_range(qh, kv, skv, seq_kv, it, 0, topk, sm_scale_log2, block_n, acc, &m, &l, qk, ks, kid);
+        mla_range(qh, kv, skv, seq_kv, it, 0, topk, sm_scale_log2, block_n, groups, acc, &m, &l, qk, ks, kid);
         float ls = l > 0.0f ? l : 1.0f;                   /* :246 */
         for (int d = 0; d < LATENT; d++) oh[d] = f32_to_bf16(acc[d] / ls);
       } else {
@@ -250,7 +285,7 @@ void oracle_sparse_mla(const uint16_t* q, int64_t sq_t, int64_t sq_h,
           int64_t end = start + split_topk < topk ? start + split_topk : topk;
           float m = NEG_LARGE, l = 0.0f;
           if (start < end) {
-            mla_range(qh, kv, skv, seq_kv, it, start, end, sm_scale_log2, block_n, acc, &m, &l, qk, ks, kid);
+            mla_range(qh, kv, skv, seq_kv, it, start, end, sm_scale_log2, block_n, groups, acc, &m, &l, qk, ks, kid);
           } else {
             for (int d = 0; d < LATENT; d++) acc[d] = 0.0f;
           }
@@ -322,4 +357,4 @@ void oracle_sparse_mla_f64(const uint16_t* q, int64_t sq_t, int64_t sq_h,
 }
 
 /* Version tag so Python can check it loaded the intended build. */
-int oracle_abi_version(void) { return 1; }
+int oracle_abi_version(void) { return 2; }
