@@ -376,6 +376,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 // Empty splits carry lse = -inf and weigh 0; no valid split gives 0.
 constexpr int kMergeLanes = 8;
 constexpr int kMaxMergeSplits = 1024;
+constexpr int kMergeRegs = 16;   // splits per lane held in registers (S <= 128)
 
 __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __restrict__ part,
                                                                const float* __restrict__ lse,
@@ -393,6 +394,20 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
   const int sl = tid >> 5;          // split lane
   const int ch = tid & 31;          // 4-latent chunk in the quarter
   const int64_t row0 = static_cast<int64_t>(t) * num_splits * heads_padded + h;
+  const int d = quarter * 128 + ch * 4;
+  // Partials of up to kMergeRegs splits per lane are requested first, so
+  // their latency overlaps the LSE loads below.
+  float4 pv[kMergeRegs];
+  const bool in_regs = num_splits <= kMergeLanes * kMergeRegs;
+  if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < kMergeRegs; j++) {
+      const int s = sl + kMergeLanes * j;
+      pv[j] = s < num_splits ? *reinterpret_cast<const float4*>(
+                                   part + (row0 + static_cast<int64_t>(s) * heads_padded) * kLatent + d)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
 
   // LSEs -> LDS, block max.
   float m = kNegLarge;
@@ -411,16 +426,26 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
 
   float den = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  const int d = quarter * 128 + ch * 4;
-#pragma unroll 4
-  for (int s = sl; s < num_splits; s += kMergeLanes) {
-    const float e = wts[s];
-    const float4 v = *reinterpret_cast<const float4*>(
-        part + (row0 + static_cast<int64_t>(s) * heads_padded) * kLatent + d);
-    acc.x += e * v.x;
-    acc.y += e * v.y;
-    acc.z += e * v.z;
-    acc.w += e * v.w;
+  if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < kMergeRegs; j++) {
+      const int s = sl + kMergeLanes * j;
+      const float e = s < num_splits ? wts[s] : 0.f;
+      acc.x += e * pv[j].x;
+      acc.y += e * pv[j].y;
+      acc.z += e * pv[j].z;
+      acc.w += e * pv[j].w;
+    }
+  } else {
+    for (int s = sl; s < num_splits; s += kMergeLanes) {
+      const float e = wts[s];
+      const float4 v = *reinterpret_cast<const float4*>(
+          part + (row0 + static_cast<int64_t>(s) * heads_padded) * kLatent + d);
+      acc.x += e * v.x;
+      acc.y += e * v.y;
+      acc.z += e * v.z;
+      acc.w += e * v.w;
+    }
   }
   part_sum[sl][ch] = acc;
   for (int s = 0; s < num_splits; s++) den += wts[s];

@@ -61,12 +61,12 @@ def lib():
         L.oracle_quantize_row.argtypes = [P, P]
         L.oracle_moe_align.argtypes = [P, I64, P, P, P]
         L.oracle_moe_align_pairwise.argtypes = [P, I64, P, P, P]
-        L.oracle_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, F, I64, I64, I64, P, I64, I64, I]
+        L.oracle_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, F, I64, I64, I64, F, P, I64, I64, I]
         L.oracle_sparse_mla.restype = None
         L.oracle_sparse_mla_f64.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, P, I]
         L.oracle_sparse_mla_f64.restype = None
         L.oracle_abi_version.restype = I
-        assert L.oracle_abi_version() == 2
+        assert L.oracle_abi_version() == 3
         _lib = L
     return _lib
 
@@ -180,10 +180,12 @@ def _mla_args(q_u16, rows, idx):
 
 
 def sparse_mla(q_u16: np.ndarray, rows: np.ndarray, idx: np.ndarray, sm_scale: float,
-               n_splits: int = 1, block_n: int = 32, nthreads: int = 1, groups: int = 1) -> np.ndarray:
+               n_splits: int = 1, block_n: int = 32, nthreads: int = 1, groups: int = 1,
+               lazy: float = 0.0) -> np.ndarray:
     """Faithful restatement: returns bf16 bits [T, H, 512].  groups > 1 deals
     each split's tiles round-robin to that many online-softmax streams merged
-    at the end (the HIP kernel's key groups); groups = 1 is the reference."""
+    by a pairwise tree; lazy > 0 moves a stream's max only when a tile exceeds
+    it by more than `lazy`.  groups = 1, lazy = 0 is the reference."""
     q_u16, rows, idx = _mla_args(q_u16, rows, idx)
     T, H, _ = q_u16.shape
     topk = idx.shape[1]
@@ -191,7 +193,8 @@ def sparse_mla(q_u16: np.ndarray, rows: np.ndarray, idx: np.ndarray, sm_scale: f
     sm_scale_log2 = np.float32(sm_scale * LOG2E)
     lib().oracle_sparse_mla(_ptr(q_u16), q_u16.strides[0] // 2, q_u16.strides[1] // 2, _ptr(rows),
                             rows.strides[0], rows.shape[0], _ptr(idx), idx.strides[0] // 4, T, H, topk,
-                            float(sm_scale_log2), int(n_splits), int(block_n), int(groups), _ptr(out),
+                            float(sm_scale_log2), int(n_splits), int(block_n), int(groups), float(lazy),
+                            _ptr(out),
                             out.strides[0] // 2, out.strides[1] // 2, nthreads)
     return out
 

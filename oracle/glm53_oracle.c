@@ -165,15 +165,19 @@ void oracle_moe_align_pairwise(const int64_t* ids, int64_t R, int32_t* sorted,
  * tiles of block_n keys exactly as _sparse_mla_compute_tile (:117-180).
  * acc (512 floats) / *m / *l receive the running accumulators.
  * With groups > 1 the tiles are dealt round-robin (tile i -> stream i % groups)
- * to independent online-softmax streams that are combined at the end in
- * stream order with base-2 rescaling (m = max m_g, acc = sum acc_g 2^(m_g - m),
- * l = sum l_g 2^(m_g - m)): the reduction structure of the HIP kernel's key
- * groups.  groups = 1 is the reference's single stream. */
+ * to independent online-softmax streams that are combined at the end with
+ * base-2 rescaling to the largest stream max m (acc = sum_g acc_g 2^(m_g - m),
+ * l likewise, summed in stream order): the reduction structure of the HIP
+ * kernel's wavefronts.  groups = 1 is the reference's single stream.
+ * lazy > 0: a stream moves its reference max only when a tile's max exceeds
+ * it by more than `lazy` (base-2 units), to that tile's max; p = 2^(s - m_ref)
+ * can then reach 2^lazy.  lazy = 0 is the reference (:171-174). */
 static void mla_stream(const float* qf, const uint8_t* kv, int64_t skv,
                        int64_t seq_kv, const int32_t* idx, int64_t start,
                        int64_t end, float sm_scale_log2, int64_t block_n,
-                       int64_t groups, int64_t gsel, float* acc, float* m_out,
-                       float* l_out, float* qk, float* kscale, int32_t* kid) {
+                       int64_t groups, int64_t gsel, float lazy, float* acc,
+                       float* m_out, float* l_out, float* qk, float* kscale,
+                       int32_t* kid) {
   float e_max = NEG_LARGE, e_sum = 0.0f;
   for (int d = 0; d < LATENT; d++) acc[d] = 0.0f;
   int64_t tile = 0;
@@ -198,7 +202,7 @@ static void mla_stream(const float* qf, const uint8_t* kv, int64_t skv,
       kscale[j] = sc;
       if (s > tile_max) tile_max = s;
     }
-    float n_e_max = tile_max > e_max ? tile_max : e_max;  /* :171 */
+    float n_e_max = tile_max > e_max + lazy ? tile_max : e_max;  /* :171 */
     float re_scale = exp2f(e_max - n_e_max);              /* :172 */
     for (int d = 0; d < LATENT; d++) acc[d] *= re_scale;  /* :174 */
     float psum = 0.0f;
@@ -220,30 +224,39 @@ static void mla_stream(const float* qf, const uint8_t* kv, int64_t skv,
 static void mla_range(const uint16_t* qh, const uint8_t* kv, int64_t skv,
                       int64_t seq_kv, const int32_t* idx, int64_t start,
                       int64_t end, float sm_scale_log2, int64_t block_n,
-                      int64_t groups, float* acc, float* m_out, float* l_out,
-                      float* qk, float* kscale, int32_t* kid) {
+                      int64_t groups, float lazy, float* acc, float* m_out,
+                      float* l_out, float* qk, float* kscale, int32_t* kid) {
   float qf[LATENT];
   for (int d = 0; d < LATENT; d++) qf[d] = bf16_to_f32(qh[d]);
   if (groups <= 1) {
-    mla_stream(qf, kv, skv, seq_kv, idx, start, end, sm_scale_log2, block_n, 1, 0, acc, m_out,
-               l_out, qk, kscale, kid);
+    mla_stream(qf, kv, skv, seq_kv, idx, start, end, sm_scale_log2, block_n, 1, 0, lazy, acc,
+               m_out, l_out, qk, kscale, kid);
     return;
   }
-  float gacc[LATENT];
-  float m = NEG_LARGE, l = 0.0f;
-  for (int d = 0; d < LATENT; d++) acc[d] = 0.0f;
-  for (int64_t gsel = 0; gsel < groups; gsel++) {
-    float mg, lg;
-    mla_stream(qf, kv, skv, seq_kv, idx, start, end, sm_scale_log2, block_n, groups, gsel, gacc,
-               &mg, &lg, qk, kscale, kid);
-    float mm = mg > m ? mg : m;
-    float a_old = exp2f(m - mm), a_new = exp2f(mg - mm);
-    for (int d = 0; d < LATENT; d++) acc[d] = acc[d] * a_old + gacc[d] * a_new;
-    l = l * a_old + lg * a_new;
-    m = mm;
+  float* gacc = (float*)malloc((size_t)groups * LATENT * sizeof(float));
+  float* gm = (float*)malloc((size_t)groups * sizeof(float));
+  float* gl = (float*)malloc((size_t)groups * sizeof(float));
+  for (int64_t gsel = 0; gsel < groups; gsel++)
+    mla_stream(qf, kv, skv, seq_kv, idx, start, end, sm_scale_log2, block_n, groups, gsel, lazy,
+               gacc + gsel * LATENT, gm + gsel, gl + gsel, qk, kscale, kid);
+  /* flat merge: m = max m_g, acc = sum_g acc_g 2^(m_g - m), l likewise, g in order */
+  float mm = NEG_LARGE;
+  for (int64_t i = 0; i < groups; i++) mm = gm[i] > mm ? gm[i] : mm;
+  float ll = 0.0f;
+  float* out = (float*)calloc(LATENT, sizeof(float));
+  for (int64_t i = 0; i < groups; i++) {
+    float f = exp2f(gm[i] - mm);
+    for (int d = 0; d < LATENT; d++) out[d] += gacc[i * LATENT + d] * f;
+    ll += gl[i] * f;
   }
-  *m_out = m;
-  *l_out = l;
+  memcpy(gacc, out, LATENT * sizeof(float));
+  free(out);
+  gm[0] = mm;
+  gl[0] = ll;
+  memcpy(acc, gacc, LATENT * sizeof(float));
+  *m_out = gm[0];
+  *l_out = gl[0];
+  free(gacc); free(gm); free(gl);
 }
 
 /* q: bf16 [T, H, 512] with strides sq_t, sq_h (elements); kv: byte base of
@@ -251,13 +264,15 @@ static void mla_range(const uint16_t* qh, const uint8_t* kv, int64_t skv,
  * si_t; out: bf16 [T, H, 512] with strides so_t, so_h.  n_splits >= 1 follows
  * the split-KV + merge path (:258-429) when > 1, the single pass (:185-255)
  * when 1.  block_n is the tile width of the online softmax; groups > 1 deals
- * the tiles of each split to that many streams (see mla_range). */
+ * the tiles of each split to that many streams and lazy > 0 delays max
+ * updates (see mla_stream / mla_range). */
 void oracle_sparse_mla(const uint16_t* q, int64_t sq_t, int64_t sq_h,
                        const uint8_t* kv, int64_t skv, int64_t seq_kv,
                        const int32_t* idx, int64_t si_t, int64_t T, int64_t H,
                        int64_t topk, float sm_scale_log2, int64_t n_splits,
-                       int64_t block_n, int64_t groups, uint16_t* out,
-                       int64_t so_t, int64_t so_h, int nthreads) {
+                       int64_t block_n, int64_t groups, float lazy,
+                       uint16_t* out, int64_t so_t, int64_t so_h,
+                       int nthreads) {
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
 #pragma omp parallel for collapse(2) schedule(dynamic) if (nthreads != 1)
@@ -273,7 +288,7 @@ void oracle_sparse_mla(const uint16_t* q, int64_t sq_t, int64_t sq_h,
       uint16_t* oh = out + t * so_t + h * so_h;
       if (n_splits <= 1) {
         float m, l;
-        mla_range(qh, kv, skv, seq_kv, it, 0, topk, sm_scale_log2, block_n, groups, acc, &m, &l, qk, ks, kid);
+        mla_range(qh, kv, skv, seq_kv, it, 0, topk, sm_scale_log2, block_n, groups, lazy, acc, &m, &l, qk, ks, kid);
         float ls = l > 0.0f ? l : 1.0f;                   /* :246 */
         for (int d = 0; d < LATENT; d++) oh[d] = f32_to_bf16(acc[d] / ls);
       } else {
@@ -285,7 +300,7 @@ void oracle_sparse_mla(const uint16_t* q, int64_t sq_t, int64_t sq_h,
           int64_t end = start + split_topk < topk ? start + split_topk : topk;
           float m = NEG_LARGE, l = 0.0f;
           if (start < end) {
-            mla_range(qh, kv, skv, seq_kv, it, start, end, sm_scale_log2, block_n, groups, acc, &m, &l, qk, ks, kid);
+            mla_range(qh, kv, skv, seq_kv, it, start, end, sm_scale_log2, block_n, groups, lazy, acc, &m, &l, qk, ks, kid);
           } else {
             for (int d = 0; d < LATENT; d++) acc[d] = 0.0f;
           }
@@ -357,4 +372,4 @@ void oracle_sparse_mla_f64(const uint16_t* q, int64_t sq_t, int64_t sq_h,
 }
 
 /* Version tag so Python can check it loaded the intended build. */
-int oracle_abi_version(void) { return 2; }
+int oracle_abi_version(void) { return 3; }

@@ -1,7 +1,8 @@
 """GPU parity of triton_mla_sparse_attention (HIP) against the CPU oracle.
 
 Bar (BF16 attention output), against the oracle's faithful restatement run
-with the kernel's split count, tile width (32) and key groups (2):
+with the kernel's split count and reduction structure (32-key tiles dealt
+alternately to two key-group streams, merged at the end):
   per element |err| <= max(2e-2, one bf16 ulp of the reference value), and
   mean-abs <= 2e-3.
 Below |out| = 4 the per-element bound is exactly 2e-2; above it a single bf16
@@ -20,7 +21,9 @@ pytestmark = pytest.mark.gpu
 
 MAX_ABS = 2e-2
 MEAN_ABS = 2e-3
-GROUPS = 2      # key groups of the HIP kernel (independent online-softmax streams per split)
+GROUPS = 2      # key groups of the HIP kernel: independent online-softmax streams per split
+BLOCK = 32      # keys per tile
+LAZY = 0.0      # the running max moves on every increase, as in the reference
 
 
 def u16(t):
@@ -84,7 +87,7 @@ def test_small_b1_splits(cuda, oracle, small_cache, splits):
     out = triton_mla_sparse_attention(w["q"], w["cache"].view(n, 1, 528), w["idx"], W.SM_SCALE,
                                       num_kv_splits=splits)
     torch.cuda.synchronize()
-    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS)
+    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
     mx, mean = compare(out, want, f"splits={splits}")
     assert mean < 1e-4        # ~bf16 ulp-level agreement
 
@@ -97,7 +100,7 @@ def test_small_auto_splits_and_graph(cuda, oracle, small_cache):
     kv = w["cache"].view(n, 1, 528)
     out = triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE)
     s = _choose_num_kv_splits_mi355x(1, 1, 2176, torch.cuda.get_device_properties(0).multi_processor_count)
-    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=s, groups=GROUPS)
+    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=s, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
     compare(out, want, "auto")
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -177,7 +180,7 @@ def test_head_counts_and_edges(cuda, oracle, small_cache):
         idx = torch.randint(-50, n + 50, (3, 1, topk), generator=g, device=cuda, dtype=torch.int32)
         out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
         torch.cuda.synchronize()
-        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS)
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
         compare(out, want, (heads, topk, splits))
     # int64 indices, including values that alias valid rows modulo 2^32
     q = torch.randn(2, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
@@ -185,7 +188,7 @@ def test_head_counts_and_edges(cuda, oracle, small_cache):
     idx64[0, 0, :40] += 1 << 32
     out = triton_mla_sparse_attention(q, kv, idx64, W.SM_SCALE, num_kv_splits=2)
     clean = torch.where((idx64 >= 0) & (idx64 < n), idx64, -1).to(torch.int32)
-    want = oracle.sparse_mla(u16(q), rows, clean.cpu().numpy(), W.SM_SCALE, n_splits=2, groups=GROUPS)
+    want = oracle.sparse_mla(u16(q), rows, clean.cpu().numpy(), W.SM_SCALE, n_splits=2, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
     compare(out, want, "int64")
     # no tokens
     empty = triton_mla_sparse_attention(q[:0], kv, idx64[:0].to(torch.int32), W.SM_SCALE)
@@ -219,7 +222,7 @@ def test_full_context_b1_b8(cuda, oracle, full_cache):
             torch.cuda.synchronize()
             s = splits or _choose_num_kv_splits_mi355x(q.shape[0], 1, 2176, cu)
             want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s,
-                                     nthreads=oracle.default_threads(), groups=GROUPS)
+                                     nthreads=oracle.default_threads(), groups=GROUPS, block_n=BLOCK, lazy=LAZY)
             compare(out, want, (name, splits))
             ref64 = oracle.sparse_mla_f64(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE,
                                           nthreads=oracle.default_threads())
@@ -243,6 +246,6 @@ def test_prefill_shaped_sampled(cuda, oracle, full_cache):
     qs = u16(q)[pick]
     ids = idx.cpu().numpy()[pick]
     want = oracle.sparse_mla(qs, rows, ids, W.SM_SCALE, n_splits=1, nthreads=oracle.default_threads(),
-                             groups=GROUPS)
+                             groups=GROUPS, block_n=BLOCK, lazy=LAZY)
     got = out[torch.as_tensor(pick, device=cuda)]
     compare(got, want, "prefill sample")

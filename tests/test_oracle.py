@@ -244,15 +244,18 @@ def test_mla_faithful_vs_textbook(oracle, splits):
 
 
 @pytest.mark.parametrize("splits", [1, 8])
-def test_mla_key_groups_match_single_stream(oracle, splits):
-    """The HIP kernel deals each split's tiles to 2 online-softmax streams
-    merged at the end; that reduction order agrees with the reference's single
-    stream (and with textbook attention) to the output bar."""
+@pytest.mark.parametrize("groups,block_n,lazy", [(2, 32, 0.0), (4, 16, 8.0)])
+def test_mla_key_groups_match_single_stream(oracle, splits, groups, block_n, lazy):
+    """Tiles dealt to several online-softmax streams (the HIP kernel's key
+    groups; also with a lazily moved max) merged at the end agree with the
+    reference's single stream, and with textbook attention, to the output
+    bar."""
     from oracle import bf16_to_f32
     for dist in ("normal", "t3"):
         q, rows, idx = _mla_case(oracle, T=3, topk=2176, pad=128, dist=dist, seed=9)
         one = bf16_to_f32(oracle.sparse_mla(q, rows, idx, 512 ** -0.5, n_splits=splits))
-        two = bf16_to_f32(oracle.sparse_mla(q, rows, idx, 512 ** -0.5, n_splits=splits, groups=2))
+        two = bf16_to_f32(oracle.sparse_mla(q, rows, idx, 512 ** -0.5, n_splits=splits, groups=groups,
+                                            block_n=block_n, lazy=lazy))
         err = np.abs(one - two)
         ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(one), 2.0 ** -126))) - 7)
         assert np.all(err <= np.maximum(2e-2, ulp)) and err.mean() < 2e-4, dist
