@@ -32,13 +32,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // Wave-uniform value in a scalar register.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Maximum over the wave, returned to every lane, without LDS traffic: DPP
+// quad permutes and row rotations inside each 16-lane row, then
+// v_permlane16_swap / v_permlane32_swap across the four rows.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    uint32_t other = (uint32_t)__shfl_xor((int)v, o, 64);
-    v = v > other ? v : other;
-  }
-  return v;
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false)));   // lane ^ 1
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4E, 0xF, 0xF, false)));   // lane ^ 2
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x124, 0xF, 0xF, false)));  // row_ror 4
+  v = mx(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x128, 0xF, 0xF, false)));  // row_ror 8
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = mx(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return mx(b[0], b[1]);
 }
 
 }  // namespace glm53

@@ -7,11 +7,13 @@
 // skipped, and so is a slot at or beyond the cache capacity (the reference
 // leaves that case undefined).
 //
-// Layout: one wavefront per row.  Lane i loads bf16 elements [8i, 8i+8) as
-// one 16-byte load and stores their 8 int8 codes as one 8-byte store; lane 0
-// stores the 16-byte tail [s, 0, 0, 0].  max|x| is taken on the bf16 bit
-// patterns (|x| = bits & 0x7fff orders like the values for finite inputs)
-// and reduced across the wave.
+// Layout: a wavefront handles 2 rows, both loaded before either is reduced.
+// Lane i loads bf16 elements [8i, 8i+8) of a row as one 16-byte
+// non-temporal load (the latents stream through once) and stores their 8
+// int8 codes as one 8-byte store; lane 0 stores the 16-byte tail
+// [s, 0, 0, 0].  max|x| is taken on the bf16 bit patterns (|x| = bits &
+// 0x7fff orders like the values for finite inputs) and reduced across the
+// wave with DPP and permlane swaps (no LDS traffic).
 //
 // Quotient: the reference rounds the IEEE quotient fl(x / s) to an integer.
 // Instead of a full division per element the kernel takes y = fl(1 / s) once
@@ -113,8 +115,8 @@ __global__ __launch_bounds__(256) void store_int8_vec(const uint16_t* __restrict
       b[2 * k + 1] = quant_bits(__uint_as_float(w[k] & 0xffff0000u), s, y);
     }
     uint8_t* dst = cache + (slot[r] / block) * cs0 + (slot[r] % block) * cs1;
-    uint2 out = make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
-    reinterpret_cast<uint2*>(dst)[lane] = out;
+    reinterpret_cast<uint2*>(dst)[lane] =
+        make_uint2(pack4(b[0], b[1], b[2], b[3]), pack4(b[4], b[5], b[6], b[7]));
     if (lane == 0)
       *reinterpret_cast<uint4*>(dst + kLatent) = make_uint4(__float_as_uint(s), 0u, 0u, 0u);
   }
@@ -174,7 +176,7 @@ extern "C" int glm53_store_int8(const void* x, int64_t x_row_stride, void* cache
   const auto* xp = static_cast<const uint16_t*>(x);
   auto* cp = static_cast<uint8_t*>(cache);
   if (aligned) {
-    constexpr int kRows = 2;
+    constexpr int kRows = 2;   // measured best of 1/2/4/8 rows per wave on MI355X
     const int64_t rows_per_block = kWavesPerBlock * kRows;
     const int64_t grid = (n_slots + rows_per_block - 1) / rows_per_block;
     if (grid > 0x7fffffff) return GLM53_ERR_BAD_SHAPE;
