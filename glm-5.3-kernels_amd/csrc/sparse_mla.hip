@@ -46,6 +46,7 @@ constexpr int kSlice = kLatent / kSlices;
 constexpr int kVStride = kSlice + 16;  // bf16 per LDS row: 288 bytes, rows 8 banks apart
 constexpr int kChunkTiles = 8;         // tiles whose gathers are in flight together
 constexpr int kRounds = kChunkTiles / kGroups;
+constexpr int kRowStride = kLatent + 4;  // fp32 per LDS result row: 16 rows hit 64 distinct banks
 constexpr float kNegLarge = -1.0e30f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -68,6 +69,7 @@ struct MlaArgs {
   uint16_t* out;
   int64_t so_t, so_h;
   int partials_only;   // write part/lse even for a single split
+  int out_align16;     // out rows 16-byte aligned (else 8-byte stores)
 };
 
 __device__ __forceinline__ float f4_get(const float4& v, int i) {
@@ -119,9 +121,9 @@ struct __attribute__((aligned(16))) MlaShared {
   union {
     uint16_t vbuf[kWaves][kTile][kVStride];          // per-wave bf16 V slice of a tile
     struct {
-      float acc[kSlices][32][64];                      // key group 1's accumulators
-      float ml[kHeads][2];                             // key group 1's (m, l) per head
-    } merge;
+      float rows[kGroups][kHeads][kRowStride];         // each key group's acc, row-major
+      float ml[kGroups][kHeads][2];                    // each key group's (m, l) per head
+    } fin;
   };
   float red[2][kGroups][kSlices][64][8];               // partial S^T per slice
   float scl[2][kChunkTiles][kTile];                    // row scales of the chunk
@@ -312,58 +314,69 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
     }
   }
 
-  // ---- merge key group 1 into key group 0 (vbuf is free after the barrier).
-  __syncthreads();
-  if (kg == 1) {
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) sh.merge.acc[sl][4 * dt + i][lane] = acc[dt][i];
-    }
-    if (sl == 0 && g == 0) {
-      sh.merge.ml[c][0] = m_run;
-      sh.merge.ml[c][1] = l_run;
-    }
-  }
-  __syncthreads();
-  if (kg == 1 || !head_ok) return;
+  // ---- combine the two key groups and write the 16 result rows.  The MFMA
+  // C layout scatters a lane's values over 16 rows (16 x 64-byte pieces per
+  // store instruction, which the memory pipeline issues ~2.5x slower than
+  // contiguous ones), so both key groups park their accumulators row-major
+  // in LDS and every wave then finishes two whole rows with contiguous
+  // 1 KB stores.
+  __syncthreads();  // vbuf is free
   {
-    const float m1 = sh.merge.ml[c][0];
-    const float l1 = sh.merge.ml[c][1];
-    const float mm = fmaxf(m_run, m1);
-    const float a0 = fast_exp2(m_run - mm);
-    const float a1 = fast_exp2(m1 - mm);
+    float* rp = &sh.fin.rows[kg][c][kSlice * sl + 4 * g];
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-#pragma unroll
-      for (int i = 0; i < 4; i++) acc[dt][i] = acc[dt][i] * a0 + sh.merge.acc[sl][4 * dt + i][lane] * a1;
+    for (int dt = 0; dt < 8; dt++)
+      *reinterpret_cast<float4*>(rp + 16 * dt) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+    if (sl == 0 && g == 0) {
+      sh.fin.ml[kg][c][0] = m_run;
+      sh.fin.ml[kg][c][1] = l_run;
     }
-    l_run = l_run * a0 + l1 * a1;
-    m_run = mm;
   }
-
-  // 1 / l once, then multiplies (the reference divides; the two differ by at
-  // most one fp32 ulp before the bf16 / fp32 store).
-  const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
-  if (a.num_splits == 1 && !a.partials_only) {
-    uint16_t* op = a.out + t * a.so_t + head * a.so_h + kSlice * sl + 4 * g;
+  __syncthreads();
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-      uint2 o;
-      o.x = pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l);
-      o.y = pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l);
-      *reinterpret_cast<uint2*>(op + 16 * dt) = o;
+  for (int k = 0; k < kHeads / kWaves; k++) {
+    const int r = (kHeads / kWaves) * w + k;   // result row (head in the group), uniform per wave
+    const int hd = hg * kHeads + r;
+    if (hd >= a.num_heads) break;
+    const float m0 = sh.fin.ml[0][r][0], l0 = sh.fin.ml[0][r][1];
+    const float m1 = sh.fin.ml[1][r][0], l1 = sh.fin.ml[1][r][1];
+    const float mm = fmaxf(m0, m1);
+    const float a0 = fast_exp2(m0 - mm);
+    const float a1 = fast_exp2(m1 - mm);
+    const float l = l0 * a0 + l1 * a1;
+    // 1 / l once, then multiplies (the reference divides; the two differ by
+    // at most one fp32 ulp before the bf16 / fp32 store).
+    const float inv_l = 1.f / (l > 0.f ? l : 1.f);
+    const float* r0 = sh.fin.rows[0][r];
+    const float* r1 = sh.fin.rows[1][r];
+    auto fin4 = [&](int col) {
+      const float4 x0 = *reinterpret_cast<const float4*>(r0 + col);
+      const float4 x1 = *reinterpret_cast<const float4*>(r1 + col);
+      return make_float4((x0.x * a0 + x1.x * a1) * inv_l, (x0.y * a0 + x1.y * a1) * inv_l,
+                         (x0.z * a0 + x1.z * a1) * inv_l, (x0.w * a0 + x1.w * a1) * inv_l);
+    };
+    if (a.num_splits == 1 && !a.partials_only) {
+      // lane: latents [8 lane, 8 lane + 8) -> one 16-byte bf16 store
+      const float4 u = fin4(8 * lane);
+      const float4 v = fin4(8 * lane + 4);
+      uint4 o;
+      o.x = pack_bf16x2(u.x, u.y);
+      o.y = pack_bf16x2(u.z, u.w);
+      o.z = pack_bf16x2(v.x, v.y);
+      o.w = pack_bf16x2(v.z, v.w);
+      uint16_t* op = a.out + t * a.so_t + hd * a.so_h + 8 * lane;
+      if (a.out_align16) {
+        *reinterpret_cast<uint4*>(op) = o;
+      } else {
+        reinterpret_cast<uint2*>(op)[0] = make_uint2(o.x, o.y);
+        reinterpret_cast<uint2*>(op)[1] = make_uint2(o.z, o.w);
+      }
+    } else {
+      const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + hd;
+      float* pp = a.part + row * kLatent;
+      *reinterpret_cast<float4*>(pp + 4 * lane) = fin4(4 * lane);
+      *reinterpret_cast<float4*>(pp + 256 + 4 * lane) = fin4(256 + 4 * lane);
+      if (lane == 0) a.lse[row] = (mm + log2f(l)) * kLn2;
     }
-  } else {
-    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
-    float* pp = a.part + row * kLatent + kSlice * sl + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-      float4 o = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l, acc[dt][2] * inv_l,
-                             acc[dt][3] * inv_l);
-      *reinterpret_cast<float4*>(pp + 16 * dt) = o;
-    }
-    if (sl == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
   }
 }
 
@@ -509,6 +522,7 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
   a.lse = nullptr;
   a.out = nullptr;
   a.partials_only = 0;
+  a.out_align16 = 0;
   a.so_t = a.so_h = 0;
   return 0;
 }
@@ -564,6 +578,7 @@ extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const
   a.out = static_cast<uint16_t*>(out);
   a.so_t = so_t;
   a.so_h = so_h;
+  a.out_align16 = reinterpret_cast<uintptr_t>(out) % 16 == 0 && so_t % 8 == 0 && so_h % 8 == 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   (void)hipGetLastError();
   launch_attention(a, num_tokens, st);
