@@ -46,6 +46,8 @@ constexpr int kSlice = kLatent / kSlices;
 constexpr int kVStride = kSlice + 16;  // bf16 per LDS row: 288 bytes, rows 8 banks apart
 constexpr int kChunkTiles = 8;         // tiles whose gathers are in flight together
 constexpr int kRounds = kChunkTiles / kGroups;
+constexpr int kMergeLanes = 8;         // split lanes per output chunk in the LSE merge
+constexpr int kMaxMergeSplits = 1024;
 constexpr int kRowStride = kLatent + 4;  // fp32 per LDS result row: 16 rows hit 64 distinct banks
 constexpr float kNegLarge = -1.0e30f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -382,13 +384,13 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 
 // N-way LSE merge (kernels/titan_mla.py:403-429).  One workgroup per
 // (token, head, 128-latent quarter); 256 threads = 8 split lanes x 32 chunks
-// of 4 latents.  All split LSEs are loaded at once and their maximum M taken
-// first; then out = sum_s e^{lse_s - M} part_s / sum_s e^{lse_s - M}, which is
-// the reference's running rescaled sum written without a serial dependency.
-// Split lanes are summed in a fixed order, so the result is deterministic.
-// Empty splits carry lse = -inf and weigh 0; no valid split gives 0.
-constexpr int kMergeLanes = 8;
-constexpr int kMaxMergeSplits = 1024;
+// of 4 latents.  Split lane k handles splits k, k + 8, ...: it loads their
+// partials and LSEs together (one memory round trip), the block takes the
+// maximum M of all LSEs, and each lane accumulates sum e^{lse_s - M} part_s
+// and sum e^{lse_s - M} over its splits in order; the 8 lanes are then summed
+// in a fixed order.  out = acc / den: the reference's running rescaled sum
+// written without a serial dependency, deterministic.  Empty splits carry
+// lse = -inf and weigh 0; no valid split gives 0.
 constexpr int kMergeRegs = 16;   // splits per lane held in registers (S <= 128)
 
 __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __restrict__ part,
@@ -397,8 +399,8 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
                                                                int num_heads,
                                                                uint16_t* __restrict__ out,
                                                                int64_t so_t, int64_t so_h) {
-  __shared__ float wts[kMaxMergeSplits];
   __shared__ float red_m[256 / 64];
+  __shared__ float part_den[kMergeLanes];
   __shared__ __attribute__((aligned(16))) float4 part_sum[kMergeLanes][32];
   const int t = blockIdx.x / num_heads;
   const int h = blockIdx.x % num_heads;
@@ -408,69 +410,71 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
   const int ch = tid & 31;          // 4-latent chunk in the quarter
   const int64_t row0 = static_cast<int64_t>(t) * num_splits * heads_padded + h;
   const int d = quarter * 128 + ch * 4;
-  // Partials of up to kMergeRegs splits per lane are requested first, so
-  // their latency overlaps the LSE loads below.
-  float4 pv[kMergeRegs];
   const bool in_regs = num_splits <= kMergeLanes * kMergeRegs;
+
+  float4 pv[kMergeRegs];
+  float lv[kMergeRegs];
+  float m = kNegLarge;
   if (in_regs) {
 #pragma unroll
     for (int j = 0; j < kMergeRegs; j++) {
       const int s = sl + kMergeLanes * j;
-      pv[j] = s < num_splits ? *reinterpret_cast<const float4*>(
-                                   part + (row0 + static_cast<int64_t>(s) * heads_padded) * kLatent + d)
+      const int64_t r = row0 + static_cast<int64_t>(s) * heads_padded;
+      pv[j] = s < num_splits ? *reinterpret_cast<const float4*>(part + r * kLatent + d)
                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      lv[j] = s < num_splits ? lse[r] : kNegLarge;
     }
-  }
-
-  // LSEs -> LDS, block max.
-  float m = kNegLarge;
-  for (int s = tid; s < num_splits; s += 256) {
-    const float v = lse[row0 + static_cast<int64_t>(s) * heads_padded];
-    wts[s] = v;
-    m = fmaxf(m, v);
+#pragma unroll
+    for (int j = 0; j < kMergeRegs; j++) m = fmaxf(m, lv[j]);
+  } else {
+    for (int s = sl; s < num_splits; s += kMergeLanes)
+      m = fmaxf(m, lse[row0 + static_cast<int64_t>(s) * heads_padded]);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
   if ((tid & 63) == 0) red_m[tid >> 6] = m;
   __syncthreads();
   m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
-  for (int s = tid; s < num_splits; s += 256) wts[s] = expf(wts[s] - m);
-  __syncthreads();
 
   float den = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (in_regs) {
 #pragma unroll
     for (int j = 0; j < kMergeRegs; j++) {
-      const int s = sl + kMergeLanes * j;
-      const float e = s < num_splits ? wts[s] : 0.f;
-      acc.x += e * pv[j].x;
-      acc.y += e * pv[j].y;
-      acc.z += e * pv[j].z;
-      acc.w += e * pv[j].w;
+      if (sl + kMergeLanes * j < num_splits) {
+        const float e = expf(lv[j] - m);
+        acc.x += e * pv[j].x;
+        acc.y += e * pv[j].y;
+        acc.z += e * pv[j].z;
+        acc.w += e * pv[j].w;
+        den += e;
+      }
     }
   } else {
     for (int s = sl; s < num_splits; s += kMergeLanes) {
-      const float e = wts[s];
-      const float4 v = *reinterpret_cast<const float4*>(
-          part + (row0 + static_cast<int64_t>(s) * heads_padded) * kLatent + d);
+      const int64_t r = row0 + static_cast<int64_t>(s) * heads_padded;
+      const float e = expf(lse[r] - m);
+      const float4 v = *reinterpret_cast<const float4*>(part + r * kLatent + d);
       acc.x += e * v.x;
       acc.y += e * v.y;
       acc.z += e * v.z;
       acc.w += e * v.w;
+      den += e;
     }
   }
   part_sum[sl][ch] = acc;
-  for (int s = 0; s < num_splits; s++) den += wts[s];
+  if (ch == 0) part_den[sl] = den;
   __syncthreads();
   if (sl == 0) {
     float4 r = part_sum[0][ch];
+    float dsum = part_den[0];
 #pragma unroll
     for (int k = 1; k < kMergeLanes; k++) {
       const float4 v = part_sum[k][ch];
       r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
+      dsum += part_den[k];
     }
-    const float inv = 1.f / (den > 0.f ? den : 1.f);
+    const float inv = 1.f / (dsum > 0.f ? dsum : 1.f);
     uint2 o;
     o.x = pack_bf16x2(r.x * inv, r.y * inv);
     o.y = pack_bf16x2(r.z * inv, r.w * inv);
