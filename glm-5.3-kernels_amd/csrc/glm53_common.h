@@ -24,9 +24,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
-// Pack two fp32 into a dword of two bf16 (lo in bits 0..15), RNE.
+// Pack two fp32 into a dword of two bf16 (lo in bits 0..15), round to
+// nearest even: one v_cvt_pk_bf16_f32 on gfx950 (same bits as
+// f32_to_bf16_bits for finite inputs; NaN stays NaN).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 
 // Wave-uniform value in a scalar register.

@@ -170,6 +170,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegLarge, l_run = 0.f;
+  bool acc_zero = true;  // wave-uniform: no PV product accumulated yet
 
   int buf = 0, cbuf = 0;
   for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile, cbuf ^= 1) {
@@ -290,8 +291,9 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
       const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
 
       // The running max changes rarely after the first tiles: rescale only
-      // when it moved for some head of this wave (alpha == 1 otherwise).
-      if (__ballot(alpha != 1.f)) {
+      // when it moved for some head of this wave (alpha == 1 otherwise), and
+      // not before the wave's first PV product (acc is still exactly 0).
+      if (!acc_zero && __ballot(alpha != 1.f)) {
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
           acc[dt][0] *= alpha; acc[dt][1] *= alpha; acc[dt][2] *= alpha; acc[dt][3] *= alpha;
@@ -313,6 +315,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         const uint4 vv = make_uint4(v0i[0], v0i[1], v1i[0], v1i[1]);
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, acc[dt], 0, 0, 0);
       }
+      acc_zero = false;
     }
   }
 
