@@ -244,7 +244,7 @@ def test_mla_faithful_vs_textbook(oracle, splits):
 
 
 @pytest.mark.parametrize("splits", [1, 8])
-@pytest.mark.parametrize("groups,block_n,lazy", [(2, 32, 0.0), (4, 16, 8.0)])
+@pytest.mark.parametrize("groups,block_n,lazy", [(2, 32, 0.0), (4, 32, 0.0), (4, 16, 8.0)])
 def test_mla_key_groups_match_single_stream(oracle, splits, groups, block_n, lazy):
     """Tiles dealt to several online-softmax streams (the HIP kernel's key
     groups; also with a lazily moved max) merged at the end agree with the
