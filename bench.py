@@ -239,6 +239,37 @@ def main():
                               "gbs_cold": round(bytes1 / (us1_cold * 1e-6) / 1e9, 1), "num_kv_splits": s1}
         del graph1
 
+        # ------------------------------------------------------------ paged decode B=8
+        # Request-relative indices: vLLM-style conversion + attention (two
+        # launches before the attention's own) against the fused call.
+        from sparse_utils import flat_kv_row_view, triton_convert_req_index_to_global_index
+        from titan_mla import triton_mla_sparse_attention_paged
+        pages, qpg, idxpg, reqpg, btpg = W.paged_b8_inputs(dev, g8, cache8)
+        rows_pg, stride_pg = flat_kv_row_view(pages, pages.shape[1])
+        kv_pg = rows_pg.view(-1, 1, W.ROW_BYTES)
+
+        def paged_two():
+            flat = triton_convert_req_index_to_global_index(
+                reqpg, btpg, idxpg.view(8, -1), BLOCK_SIZE=pages.shape[1], BLOCK_STRIDE_ROWS=stride_pg,
+                NUM_TOPK_TOKENS=idxpg.shape[-1])
+            return triton_mla_sparse_attention(qpg, kv_pg, flat.view(8, 1, -1), W.SM_SCALE,
+                                               num_kv_splits=args.splits)
+
+        paged_one = lambda: triton_mla_sparse_attention_paged(qpg, pages, idxpg, reqpg, btpg, W.SM_SCALE,
+                                                              num_kv_splits=args.splits)
+        log("decode_b8 paged")
+        gp2, _ = capture(torch, paged_two, args.unroll)
+        gp1, _ = capture(torch, paged_one, args.unroll)
+        for _ in range(Wm):
+            gp2.replay()
+            gp1.replay()
+        us_two = timer.replay_loop(gp2, K // args.unroll) / args.unroll
+        us_one = timer.replay_loop(gp1, K // args.unroll) / args.unroll
+        extra["decode_b8_paged"] = {"us_per_step_fused": round(us_one, 3),
+                                    "us_per_step_convert_then_attend": round(us_two, 3),
+                                    "block_size": pages.shape[1], "context_per_request": 32768}
+        del gp1, gp2
+
         # ------------------------------------------------------------ MoE align
         moe = {}
         gm = W.gen(dev, W.SEED_BENCH)

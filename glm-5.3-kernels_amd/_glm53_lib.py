@@ -18,6 +18,8 @@ EXPORTED = (
     "glm53_store_int8",
     "glm53_sparse_mla_workspace_bytes",
     "glm53_sparse_mla",
+    "glm53_convert_req_index",
+    "glm53_sparse_mla_paged",
     "glm53_sparse_mla_partials_bytes",
     "glm53_sparse_mla_partials",
     "glm53_sparse_mla_merge",
@@ -49,6 +51,11 @@ def load():
     L.glm53_sparse_mla.restype = I
     L.glm53_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, I64, P, I64,
                                    P, I64, I64, P]
+    L.glm53_convert_req_index.restype = I
+    L.glm53_convert_req_index.argtypes = [P, P, I64, I64, I64, P, I64, P, I64, I64, I64, I64, I64, P]
+    L.glm53_sparse_mla_paged.restype = I
+    L.glm53_sparse_mla_paged.argtypes = [P, I64, I64, P, I64, I64, P, I64, P, P, I64, I64, I64, I64, I64,
+                                         I64, I64, I64, D, I64, P, I64, P, I64, I64, P]
     L.glm53_sparse_mla_partials_bytes.restype = I64
     L.glm53_sparse_mla_partials_bytes.argtypes = [I64, I64, I64]
     L.glm53_sparse_mla_partials.restype = I

@@ -72,6 +72,15 @@ struct MlaArgs {
   int64_t so_t, so_h;
   int partials_only;   // write part/lse even for a single split
   int out_align16;     // out rows 16-byte aligned (else 8-byte stores)
+  // Paged indices (sparse_mla_kernel<true>): idx holds request-relative
+  // token positions, mapped to flat cache rows by to_flat_row.
+  const int32_t* req_id;   // [T] request of each query token
+  const int32_t* bt;       // block table, row r at bt + r * bt_stride
+  int64_t bt_stride;
+  int max_blocks;          // entries per block-table row
+  int num_reqs;            // block-table rows: other request ids map to -1
+  int block_size;          // tokens per cache block
+  int page_rows;           // rows per physical page in the flat row view
 };
 
 __device__ __forceinline__ float f4_get(const float4& v, int i) {
@@ -131,6 +140,25 @@ struct __attribute__((aligned(16))) MlaShared {
   float scl[2][kChunkTiles][kTile];                    // row scales of the chunk
 };
 
+// Request-relative token position -> flat cache row, the conversion vLLM's
+// triton_convert_req_index_to_global_index performs before the reference's
+// attention call (integration/titan_backend.py:48-52): a negative position,
+// or one whose block lies beyond the block-table row, gives -1; otherwise
+// block_table[req][pos / block_size] * page_rows + pos % block_size, in
+// wrapping 32-bit arithmetic like the Triton kernel.  page_rows is the
+// padded page's row count in the flat view (BLOCK_STRIDE_ROWS; block_size
+// when pages are unpadded).
+__device__ __forceinline__ int to_flat_row(const int32_t* bt_req, int max_blocks, int block_size,
+                                           int page_rows, int pos) {
+  if (pos < 0) return -1;
+  const int blk = pos / block_size;
+  if (blk >= max_blocks) return -1;
+  const int off = pos - blk * block_size;
+  return static_cast<int>(static_cast<uint32_t>(bt_req[blk]) * static_cast<uint32_t>(page_rows) +
+                          static_cast<uint32_t>(off));
+}
+
+template <bool kPaged>
 __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   __shared__ MlaShared sh;
 
@@ -148,6 +176,11 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   const int head = hg * kHeads + c;
   const bool head_ok = head < a.num_heads;
   const int32_t* idx_t = a.idx + t * a.si_t;
+  // A request id outside the block table maps every index to -1.
+  const int req = kPaged ? a.req_id[t] : 0;
+  const bool req_ok = req >= 0 && req < a.num_reqs;
+  const int32_t* bt_req = kPaged && req_ok ? a.bt + static_cast<int64_t>(req) * a.bt_stride : a.bt;
+  const int max_blocks = req_ok ? a.max_blocks : 0;
 
   // Q^T fragment (B operand of S^T = K Q^T): head c, latents
   // [128 sl + 32g, +32) -> four K-steps of 8.
@@ -181,6 +214,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
     for (int r = 0; r < kRounds; r++) {
       const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
       int v = pos < end ? idx_t[pos] : -1;
+      if (kPaged) v = to_flat_row(bt_req, max_blocks, a.block_size, a.page_rows, v);
       if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv) v = -1;
       id[r] = v;
     }
@@ -385,6 +419,26 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   }
 }
 
+// Standalone conversion (the vLLM helper the reference's adapter calls):
+// out[t][k] = to_flat_row(block_table[req_id[t]], ..., indices[t][k]).
+__global__ __launch_bounds__(256) void convert_req_index_kernel(const int32_t* __restrict__ req_id,
+                                                                const int32_t* __restrict__ bt,
+                                                                int64_t bt_stride, int max_blocks,
+                                                                int num_reqs,
+                                                                const int32_t* __restrict__ idx,
+                                                                int64_t si_t, int32_t* __restrict__ out,
+                                                                int64_t so_t, int topk, int block_size,
+                                                                int page_rows) {
+  const int t = blockIdx.y;
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= topk) return;
+  const int req = req_id[t];
+  const bool req_ok = req >= 0 && req < num_reqs;   // other ids: every index maps to -1
+  const int32_t* bt_req = req_ok ? bt + static_cast<int64_t>(req) * bt_stride : bt;
+  out[t * so_t + k] = to_flat_row(bt_req, req_ok ? max_blocks : 0, block_size, page_rows,
+                                  idx[t * si_t + k]);
+}
+
 // N-way LSE merge (kernels/titan_mla.py:403-429).  One workgroup per
 // (token, head, 128-latent quarter); 256 threads = 8 split lanes x 32 chunks
 // of 4 latents.  Split lane k handles splits k, k + 8, ...: it loads their
@@ -530,6 +584,13 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
   a.out = nullptr;
   a.partials_only = 0;
   a.out_align16 = 0;
+  a.req_id = nullptr;
+  a.bt = nullptr;
+  a.bt_stride = 0;
+  a.max_blocks = 0;
+  a.num_reqs = 0;
+  a.block_size = 1;
+  a.page_rows = 1;
   a.so_t = a.so_h = 0;
   return 0;
 }
@@ -537,7 +598,10 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
 void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
                   static_cast<unsigned>(a.heads_padded / kHeads));
-  hipLaunchKernelGGL(sparse_mla_kernel, grid, dim3(kThreads), 0, st, a);
+  if (a.bt != nullptr)
+    hipLaunchKernelGGL(sparse_mla_kernel<true>, grid, dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(sparse_mla_kernel<false>, grid, dim3(kThreads), 0, st, a);
 }
 
 void launch_merge(const float* part, const float* lse, int64_t num_tokens, int num_splits,
@@ -564,17 +628,15 @@ extern "C" int64_t glm53_sparse_mla_partials_bytes(int64_t num_tokens, int64_t n
   return rows * kLatent * 4 + rows * 4;
 }
 
-extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
-                                int64_t skv_t, int64_t seq_kv, const int32_t* indices,
-                                int64_t si_t, int64_t num_tokens, int64_t num_heads, int64_t topk,
-                                double sm_scale, int64_t num_splits, void* workspace,
-                                int64_t workspace_bytes, void* out, int64_t so_t, int64_t so_h,
-                                void* stream) {
-  MlaArgs a;
-  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, indices, si_t, num_tokens, num_heads, topk,
-                   sm_scale, num_splits);
-  if (rc) return rc;
-  if (num_tokens == 0) return 0;
+namespace glm53 {
+namespace {
+
+// Output checks, workspace split, the attention launch and (num_splits > 1)
+// the merge launch: the common tail of glm53_sparse_mla and
+// glm53_sparse_mla_paged.
+int run_attention(MlaArgs& a, int64_t num_tokens, int64_t num_heads, int64_t num_splits,
+                  void* workspace, int64_t workspace_bytes, void* out, int64_t so_t, int64_t so_h,
+                  void* stream) {
   if (!out) return GLM53_ERR_NULL_POINTER;
   if (reinterpret_cast<uintptr_t>(out) % 8 || so_t % 4 || so_h % 4) return GLM53_ERR_MISALIGNED;
   const int64_t need = glm53_sparse_mla_workspace_bytes(num_tokens, num_heads, num_splits);
@@ -592,6 +654,85 @@ extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const
   if (num_splits > 1)
     launch_merge(a.part, a.lse, num_tokens, a.num_splits, a.heads_padded, a.num_heads, a.out, so_t,
                  so_h, st);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Checks of the paged-index arguments shared by the two paged entry points.
+int check_paged(const int32_t* req_id, const int32_t* block_table, int64_t num_reqs,
+                int64_t bt_stride, int64_t max_blocks, int64_t block_size, int64_t page_rows) {
+  if (!req_id || (!block_table && max_blocks > 0 && num_reqs > 0)) return GLM53_ERR_NULL_POINTER;
+  if (block_size < 1 || page_rows < block_size || max_blocks < 0 || bt_stride < 0 ||
+      num_reqs < 0 || block_size > 0x7fffffff || page_rows > 0x7fffffff ||
+      max_blocks > 0x7fffffff || num_reqs > 0x7fffffff)
+    return GLM53_ERR_BAD_SHAPE;
+  return 0;
+}
+
+}  // namespace
+}  // namespace glm53
+
+extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
+                                int64_t skv_t, int64_t seq_kv, const int32_t* indices,
+                                int64_t si_t, int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                double sm_scale, int64_t num_splits, void* workspace,
+                                int64_t workspace_bytes, void* out, int64_t so_t, int64_t so_h,
+                                void* stream) {
+  MlaArgs a;
+  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, indices, si_t, num_tokens, num_heads, topk,
+                   sm_scale, num_splits);
+  if (rc) return rc;
+  if (num_tokens == 0) return 0;
+  return run_attention(a, num_tokens, num_heads, num_splits, workspace, workspace_bytes, out, so_t,
+                       so_h, stream);
+}
+
+extern "C" int glm53_sparse_mla_paged(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
+                                      int64_t skv_t, int64_t seq_kv, const int32_t* req_indices,
+                                      int64_t si_t, const int32_t* req_id,
+                                      const int32_t* block_table, int64_t num_reqs,
+                                      int64_t bt_stride, int64_t max_blocks, int64_t block_size,
+                                      int64_t page_rows,
+                                      int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                      double sm_scale, int64_t num_splits, void* workspace,
+                                      int64_t workspace_bytes, void* out, int64_t so_t,
+                                      int64_t so_h, void* stream) {
+  MlaArgs a;
+  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, req_indices, si_t, num_tokens, num_heads,
+                   topk, sm_scale, num_splits);
+  if (rc) return rc;
+  if (num_tokens == 0) return 0;
+  rc = check_paged(req_id, block_table, num_reqs, bt_stride, max_blocks, block_size, page_rows);
+  if (rc) return rc;
+  a.req_id = req_id;
+  a.num_reqs = block_table ? static_cast<int>(num_reqs) : 0;
+  a.bt = block_table ? block_table : req_id;   // max_blocks == 0: never read
+  a.bt_stride = bt_stride;
+  a.max_blocks = static_cast<int>(max_blocks);
+  a.block_size = static_cast<int>(block_size);
+  a.page_rows = static_cast<int>(page_rows);
+  return run_attention(a, num_tokens, num_heads, num_splits, workspace, workspace_bytes, out, so_t,
+                       so_h, stream);
+}
+
+extern "C" int glm53_convert_req_index(const int32_t* req_id, const int32_t* block_table,
+                                       int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
+                                       const int32_t* indices, int64_t si_t, int32_t* out,
+                                       int64_t so_t, int64_t num_tokens, int64_t topk,
+                                       int64_t block_size, int64_t page_rows, void* stream) {
+  if (num_tokens < 0 || topk < 0 || num_tokens > 0x7fffffff || topk > 0x7fffffff)
+    return GLM53_ERR_BAD_SHAPE;
+  if (num_tokens == 0 || topk == 0) return 0;
+  if (!indices || !out) return GLM53_ERR_NULL_POINTER;
+  int rc = check_paged(req_id, block_table, num_reqs, bt_stride, max_blocks, block_size, page_rows);
+  if (rc) return rc;
+  if (num_tokens > 65535) return GLM53_ERR_BAD_SHAPE;   // grid y
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(convert_req_index_kernel,
+                     dim3(static_cast<unsigned>((topk + 255) / 256), static_cast<unsigned>(num_tokens)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), req_id,
+                     block_table ? block_table : req_id, bt_stride, static_cast<int>(max_blocks),
+                     block_table ? static_cast<int>(num_reqs) : 0, indices, si_t, out, so_t, static_cast<int>(topk), static_cast<int>(block_size),
+                     static_cast<int>(page_rows));
   return static_cast<int>(hipGetLastError());
 }
 

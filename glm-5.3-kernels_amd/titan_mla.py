@@ -164,6 +164,85 @@ def triton_mla_sparse_attention(
     return out
 
 
+def triton_mla_sparse_attention_paged(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    req_indices: torch.Tensor,
+    req_id_per_token: torch.Tensor,
+    block_table: torch.Tensor,
+    sm_scale: float,
+    num_kv_splits: int | None = None,
+    sm_count: int | None = None,
+) -> torch.Tensor:
+    """The adapter's two steps in one launch (integration/titan_backend.py:48-54):
+    request-relative indices are mapped to cache rows as
+    sparse_utils.triton_convert_req_index_to_global_index maps them, inside
+    the attention's index load.  Same result as converting first and calling
+    triton_mla_sparse_attention on sparse_utils.flat_kv_row_view(kv_cache).
+
+    Args:
+        q:            [T, H, 512] bf16
+        kv_cache:     int8 [num_blocks, block_size, 528] paged cache (rows
+                      contiguous; the page stride may be padded by whole rows)
+        req_indices:  int32 [T, topk] or [T, 1, topk] request-relative token
+                      positions, -1 for padding
+        req_id_per_token: int32 [T]
+        block_table:  int32 [num_reqs, max_blocks]
+    """
+    from sparse_utils import flat_kv_row_view
+    assert kv_cache.dtype == torch.int8 and kv_cache.dim() == 3 and kv_cache.shape[2] == _ROW_BYTES
+    rows, page_rows = flat_kv_row_view(kv_cache, kv_cache.shape[1])
+    if req_indices.dim() == 3:
+        assert req_indices.shape[1] == 1
+        req_indices = req_indices[:, 0, :]
+    assert req_indices.dtype == torch.int32 and req_id_per_token.dtype == torch.int32
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2
+    num_tokens, num_heads_q, dim_qk = q.shape
+    assert dim_qk == _BLOCK_DMODEL and q.dtype == torch.bfloat16
+    assert req_id_per_token.numel() == num_tokens and req_indices.shape[0] == num_tokens
+    index_topk = req_indices.shape[1]
+    assert index_topk % _MIN_BLOCK_N == 0, (
+        f"topk ({index_topk}) must be a multiple of the smallest autotune BLOCK_N ({_MIN_BLOCK_N})")
+
+    num_head_groups = triton_cdiv(num_heads_q, min(_BLOCK_H, num_heads_q))
+    if num_kv_splits is None or num_kv_splits == 0:
+        if sm_count is None:
+            sm_count = num_compute_units(q.device.index)
+        num_kv_splits = _choose_num_kv_splits_mi355x(num_tokens, num_head_groups, index_topk, sm_count)
+    if num_kv_splits < 1:
+        raise ValueError(f"num_kv_splits must be >= 1, got {num_kv_splits}")
+    out = torch.empty((num_tokens, num_heads_q, _BLOCK_DV), dtype=torch.bfloat16, device=q.device)
+    if num_tokens == 0:
+        return out
+    if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    if req_indices.stride(1) != 1:
+        req_indices = req_indices.contiguous()
+    if block_table.stride(1) != 1:
+        block_table = block_table.contiguous()
+    req_id_per_token = req_id_per_token.contiguous()
+
+    L = _lib.load()
+    ws_bytes = L.glm53_sparse_mla_workspace_bytes(num_tokens, num_heads_q, num_kv_splits)
+    workspace = (torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None)
+    with torch.cuda.device(q.device):
+        rc = L.glm53_sparse_mla_paged(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            rows.data_ptr(), rows.stride(0), rows.shape[0],
+            req_indices.data_ptr(), req_indices.stride(0),
+            req_id_per_token.data_ptr(),
+            block_table.data_ptr() if block_table.numel() else None,
+            block_table.shape[0], block_table.stride(0), block_table.shape[1],
+            kv_cache.shape[1], page_rows,
+            num_tokens, num_heads_q, index_topk,
+            float(sm_scale), num_kv_splits,
+            workspace.data_ptr() if workspace is not None else None, ws_bytes,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.stream_handle(q.device))
+    _lib.check(rc, "glm53_sparse_mla_paged")
+    return out
+
+
 def sparse_mla_partials(q, kv, indices, sm_scale, num_kv_splits):
     """First stage only: per-split normalised outputs and LSEs (fp32) in one
     buffer laid out as glm53.h documents (part [T*S*Hp, 512] then lse

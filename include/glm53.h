@@ -88,6 +88,43 @@ int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h,
                      void* stream);
 
 /*
+ * Request-relative indices.  The reference's vLLM adapter converts the
+ * indexer's request-relative token positions to flat cache rows with
+ * vLLM's triton_convert_req_index_to_global_index and then calls the
+ * attention (integration/titan_backend.py:48-54).  Mapping of one position
+ * p of query token t (req = req_id[t]):
+ *   p < 0, req outside [0, num_reqs), or p / block_size >= max_blocks -> -1;
+ *   otherwise block_table[req * bt_stride + p / block_size] * page_rows
+ *             + p % block_size   (32-bit wrapping arithmetic)
+ * page_rows (>= block_size) is the row count of one physical page in the
+ * flat row view (vLLM's BLOCK_STRIDE_ROWS; block_size for unpadded pages).
+ *
+ * glm53_convert_req_index writes the mapped rows (int32 [num_tokens, topk],
+ * row stride so_t) -- the conversion alone.
+ * glm53_sparse_mla_paged is glm53_sparse_mla with the mapping applied to
+ * each index as it is loaded (one launch fewer per decode step; results
+ * identical to converting first).  kv / skv_t / seq_kv describe the flat row
+ * view (seq_kv = physical pages * page_rows); rows outside [0, seq_kv) are
+ * masked as in glm53_sparse_mla.
+ */
+int glm53_convert_req_index(const int32_t* req_id, const int32_t* block_table,
+                            int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
+                            const int32_t* indices, int64_t si_t, int32_t* out,
+                            int64_t so_t, int64_t num_tokens, int64_t topk,
+                            int64_t block_size, int64_t page_rows, void* stream);
+int glm53_sparse_mla_paged(const void* q, int64_t sq_t, int64_t sq_h,
+                           const void* kv, int64_t skv_t, int64_t seq_kv,
+                           const int32_t* req_indices, int64_t si_t,
+                           const int32_t* req_id, const int32_t* block_table,
+                           int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
+                           int64_t block_size, int64_t page_rows,
+                           int64_t num_tokens, int64_t num_heads, int64_t topk,
+                           double sm_scale, int64_t num_splits,
+                           void* workspace, int64_t workspace_bytes,
+                           void* out, int64_t so_t, int64_t so_h,
+                           void* stream);
+
+/*
  * The two stages of glm53_sparse_mla, exposed for callers that merge split
  * results themselves (for example after gathering one token's splits from
  * several devices).  Same stages as the reference's _sparse_mla_kernel_split

@@ -11,6 +11,14 @@ pieces of reference host logic the tests need:
 * choose_num_kv_splits  -- kernels/titan_mla.py:432-449
 * moe_patterns          -- benchmarks/moe_align.py:49-55
 
+and, in numpy, the request-relative index conversion the reference's adapter
+runs before the attention (integration/titan_backend.py:48-52, vLLM's
+triton_convert_req_index_to_global_index, not available here):
+
+* convert_req_index     -- parity with vLLM unpinned; pinned by invariants
+  (identity table, page/offset decomposition, masking) and by attention over
+  the logically gathered cache (tests/test_oracle.py).
+
 Pinning (what each function is checked against, in tests/test_oracle.py):
 * store_int8: exact rational arithmetic (fractions.Fraction) on golden rows,
   closed-form special cases (zero row, amax element -> +-127, tail bytes,
@@ -213,3 +221,31 @@ def sparse_mla_f64(q_u16: np.ndarray, rows: np.ndarray, idx: np.ndarray, sm_scal
 
 def default_threads() -> int:
     return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+
+
+def convert_req_index(req_id: np.ndarray, block_table: np.ndarray, indices: np.ndarray,
+                      block_size: int, page_rows: int | None = None) -> np.ndarray:
+    """Request-relative token positions -> flat cache rows (int32).
+
+    For token t (request r = req_id[t]) and position p = indices[t, k]:
+    -1 if p < 0, r is not a block-table row, or p // block_size >= max_blocks;
+    otherwise block_table[r, p // block_size] * page_rows + p % block_size in
+    wrapping 32-bit arithmetic (page_rows defaults to block_size)."""
+    page_rows = block_size if page_rows is None else page_rows
+    req_id = np.asarray(req_id, dtype=np.int64)
+    bt = np.asarray(block_table, dtype=np.int32)
+    idx = np.asarray(indices, dtype=np.int64)
+    num_reqs, max_blocks = bt.shape
+    out = np.full(idx.shape, -1, dtype=np.int32)
+    for t in range(idx.shape[0]):
+        r = req_id[t]
+        if r < 0 or r >= num_reqs:
+            continue
+        p = idx[t]
+        blk = np.where(p >= 0, p // block_size, max_blocks)
+        ok = (p >= 0) & (blk < max_blocks)
+        base = bt[r, np.where(ok, blk, 0)].astype(np.uint32) if max_blocks else np.zeros(p.shape, np.uint32)
+        row = base * np.uint32(page_rows) + (p - np.maximum(blk, 0) * block_size).astype(np.uint32)
+        out[t] = np.where(ok, row.astype(np.uint32).view(np.int32), -1)
+    return out
+

@@ -119,7 +119,8 @@ def test_import_does_not_touch_cuda():
     with patch.dict(sys.modules, {"torch": fake_torch}):
         for fname, exported in (("titan_kv.py", "store_int8"),
                                 ("titan_mla.py", "triton_mla_sparse_attention"),
-                                ("titan_moe_align.py", "titan_moe_align_small")):
+                                ("titan_moe_align.py", "titan_moe_align_small"),
+                                ("sparse_utils.py", "triton_convert_req_index_to_global_index")):
             spec = importlib.util.spec_from_file_location("isolated_" + fname[:-3], pkg / fname)
             mod = importlib.util.module_from_spec(spec)
             spec.loader.exec_module(mod)
@@ -130,3 +131,54 @@ def test_product_does_not_import_oracle():
     for f in (ROOT / "glm-5.3-kernels_amd").rglob("*.py"):
         text = f.read_text()
         assert "import oracle" not in text and "from oracle" not in text, f
+
+
+def test_paged_entry_points_host_errors():
+    import _glm53_lib
+    L = _glm53_lib.load()
+    fake = ctypes.c_void_p(0x10000)
+    # convert: null req_id, zero block size, page rows below block size, T = 0
+    assert L.glm53_convert_req_index(None, fake, 2, 8, 8, fake, 64, fake, 64, 1, 64, 16, 16, None) == -1
+    assert L.glm53_convert_req_index(fake, fake, 2, 8, 8, fake, 64, fake, 64, 1, 64, 0, 16, None) == -2
+    assert L.glm53_convert_req_index(fake, fake, 2, 8, 8, fake, 64, fake, 64, 1, 64, 16, 15, None) == -2
+    assert L.glm53_convert_req_index(fake, fake, 2, 8, 8, fake, 64, fake, 64, 0, 64, 16, 16, None) == 0
+    # paged attention: argument errors before any launch
+    args = [fake, 8192, 512, fake, 528, 1024, fake, 2176, fake, fake, 2, 8, 8, 64, 64,
+            1, 16, 2176, 0.04, 4, None, 0, fake, 8192, 512, None]
+    assert L.glm53_sparse_mla_paged(*args) == -4                        # no workspace
+    bad = list(args); bad[8] = None
+    assert L.glm53_sparse_mla_paged(*bad) == -1                         # null req_id
+    bad = list(args); bad[13] = 0
+    assert L.glm53_sparse_mla_paged(*bad) == -2                         # block size 0
+    bad = list(args); bad[15] = 0
+    assert L.glm53_sparse_mla_paged(*bad) == 0                          # T = 0
+
+
+def test_flat_kv_row_view_on_cpu():
+    import torch
+    from sparse_utils import flat_kv_row_view
+    raw = torch.arange(5 * 7 * 3, dtype=torch.int32).reshape(5, 7, 3)
+    paged = raw[:, :4, :]                     # 4 tokens per block, pages of 7 rows
+    rows, stride = flat_kv_row_view(paged, 4)
+    assert stride == 7 and rows.shape == (4 * 7 + 4, 3)
+    for b in range(5):
+        for i in range(4):
+            assert torch.equal(rows[b * 7 + i], paged[b, i])
+    with pytest.raises(ValueError):
+        flat_kv_row_view(paged, 8)
+    with pytest.raises(ValueError):
+        flat_kv_row_view(torch.zeros(4, 4, 3)[:, :, :2], 4)   # rows not contiguous
+
+
+def test_convert_contract_on_cpu():
+    import torch
+    from sparse_utils import triton_convert_req_index_to_global_index as conv
+    req = torch.zeros(2, dtype=torch.int32)
+    bt = torch.zeros(1, 4, dtype=torch.int32)
+    idx = torch.zeros(2, 256, dtype=torch.int32)
+    with pytest.raises(AssertionError):
+        conv(req, bt, idx, BLOCK_SIZE=64, NUM_TOPK_TOKENS=128)
+    with pytest.raises(AssertionError):
+        conv(req.long(), bt, idx, BLOCK_SIZE=64, NUM_TOPK_TOKENS=256)
+    with pytest.raises(NotImplementedError):
+        conv(req, bt, idx, BLOCK_SIZE=64, NUM_TOPK_TOKENS=256, HAS_PREFILL_WORKSPACE=True)

@@ -309,3 +309,77 @@ def test_split_heuristic_hand_table(oracle):
     assert [oracle.choose_num_kv_splits(t, 1, 2176, 70) for t in (1, 6, 8, 2048)] == [32, 8, 8, 1]
     assert oracle.choose_num_kv_splits(0, 1, 2176, 70) == 1
     assert oracle.choose_num_kv_splits(1, 1, 96, 70) == 1
+
+
+# ---- request-relative index conversion (vLLM helper; parity with vLLM unpinned) ----
+
+def _paged_case(rng, num_reqs=3, block_size=16, page_rows=19, max_blocks=6, num_blocks=24):
+    """Physical pages of page_rows rows (only the first block_size hold
+    tokens), a block table of distinct pages per request."""
+    perm = rng.permutation(num_blocks)[: num_reqs * max_blocks].reshape(num_reqs, max_blocks)
+    return perm.astype(np.int32), block_size, page_rows, num_blocks
+
+
+def test_convert_identity_table(oracle):
+    """One request whose table is 0, 1, 2, ... and unpadded pages: a position
+    maps to itself; past the table, or negative, to -1."""
+    bt = np.arange(5, dtype=np.int32)[None, :]
+    p = np.array([[0, 1, 15, 16, 79, 80, 81, -1, -7, 1000]])
+    out = oracle.convert_req_index(np.array([0]), bt, p, 16)
+    assert out.tolist() == [[0, 1, 15, 16, 79, -1, -1, -1, -1, -1]]
+
+
+def test_convert_decomposes_into_page_and_offset(oracle):
+    rng = np.random.default_rng(4)
+    bt, bs, pr, nb = _paged_case(rng)
+    req = np.array([2, 0, 1, 7, -1])
+    p = rng.integers(-3, bt.shape[1] * bs + 9, size=(5, 64))
+    out = oracle.convert_req_index(req, bt, p, bs, pr)
+    for t in range(5):
+        for k in range(64):
+            valid = 0 <= req[t] < bt.shape[0] and 0 <= p[t, k] < bt.shape[1] * bs
+            if not valid:
+                assert out[t, k] == -1
+            else:
+                page, off = divmod(int(out[t, k]), pr)
+                assert page == bt[req[t], p[t, k] // bs] and off == p[t, k] % bs < bs
+
+
+def test_convert_wraps_like_int32(oracle):
+    bt = np.array([[2 ** 30 + 3]], dtype=np.int32)
+    out = oracle.convert_req_index(np.array([0]), bt, np.array([[5]]), 8, 8)
+    assert out[0, 0] == np.int32(np.uint32(((2 ** 30 + 3) * 8 + 5) % 2 ** 32).view(np.int32))
+
+
+@pytest.mark.parametrize("page_rows", [16, 19])
+def test_paged_attention_equals_logical_cache(oracle, page_rows):
+    """Attention through converted indices over the flat paged rows equals
+    attention over each request's logically ordered cache (its pages
+    concatenated in block-table order) indexed by the raw positions; a
+    slip (page stride taken as block_size with padded pages, or div / mod
+    swapped) gathers other rows and fails."""
+    from oracle import bf16_to_f32
+    rng = np.random.default_rng(11)
+    bt, bs, _, nb = _paged_case(rng, page_rows=page_rows)
+    pr = page_rows
+    lat = rng.standard_normal((nb * pr, 512))
+    flat = oracle.quantize_rows(_bf16(lat))
+    T, topk = 4, 128
+    req = np.array([1, 0, 2, 1])
+    q = _bf16(rng.standard_normal((T, 16, 512)))
+    p = rng.integers(0, bt.shape[1] * bs, size=(T, topk)).astype(np.int32)
+    p[:, -16:] = -1
+    conv = oracle.convert_req_index(req, bt, p, bs, pr)
+    via_pages = bf16_to_f32(oracle.sparse_mla(q, flat, conv, 512 ** -0.5, n_splits=2))
+    for t in range(T):
+        logical = np.concatenate([flat[bt[req[t], j] * pr: bt[req[t], j] * pr + bs] for j in range(bt.shape[1])])
+        one = bf16_to_f32(oracle.sparse_mla(q[t:t + 1], logical, p[t:t + 1], 512 ** -0.5, n_splits=2))
+        assert np.array_equal(one[0], via_pages[t]), t
+    if pr != bs:
+        slip = oracle.convert_req_index(req, bt, p, bs, bs)
+        bad = bf16_to_f32(oracle.sparse_mla(q, flat, slip, 512 ** -0.5, n_splits=2))
+        assert not np.array_equal(bad, via_pages)
+    swapped = np.where(p >= 0, (p % bs) * bs + p // bs, -1)   # div / mod swapped
+    bad2 = bf16_to_f32(oracle.sparse_mla(q, flat, oracle.convert_req_index(req, bt, swapped, bs, pr), 512 ** -0.5,
+                                         n_splits=2))
+    assert not np.array_equal(bad2, via_pages)

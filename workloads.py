@@ -121,6 +121,23 @@ def decode_b8_inputs(device, g, n_rows=262144):
     return q, idx
 
 
+def paged_b8_inputs(device, g, cache, block_size=64, context=32768):
+    """The decode_b8 shape in request-relative form: the 262144-row cache seen
+    as pages of block_size rows, 8 requests of `context` tokens each owning a
+    random set of pages (block table [8, context / block_size]), one query
+    token per request, indices request-relative positions (locality-biased
+    toward the request's end, 0..256 trailing pads)."""
+    n_rows = cache.shape[0] * cache.shape[1]
+    pages = cache.view(n_rows // block_size, block_size, ROW_BYTES)
+    per_req = context // block_size
+    bt = torch.randperm(pages.shape[0], generator=g, device=device)[: 8 * per_req]
+    bt = bt.view(8, per_req).to(torch.int32).contiguous()
+    req = torch.arange(8, device=device, dtype=torch.int32)
+    q = torch.randn(8, HEADS, LATENT, generator=g, device=device).to(torch.bfloat16)
+    idx = local_biased_indices(8, context, device, g)
+    return pages, q, idx, req, bt
+
+
 def prefill_inputs(device, g, n_rows=262144, tokens=2048):
     q = torch.randn(tokens, HEADS, LATENT, generator=g, device=device).to(torch.bfloat16)
     pos = n_rows - tokens + torch.arange(tokens, device=device)
