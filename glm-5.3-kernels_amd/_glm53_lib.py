@@ -54,7 +54,7 @@ def load():
     L.glm53_convert_req_index.restype = I
     L.glm53_convert_req_index.argtypes = [P, P, I64, I64, I64, P, I64, P, I64, I64, I64, I64, I64, P]
     L.glm53_sparse_mla_paged.restype = I
-    L.glm53_sparse_mla_paged.argtypes = [P, I64, I64, P, I64, I64, P, I64, P, P, I64, I64, I64, I64, I64,
+    L.glm53_sparse_mla_paged.argtypes = [P, I64, I64, P, I64, I64, I64, P, I64, P, P, I64, I64, I64, I64,
                                          I64, I64, I64, D, I64, P, I64, P, I64, I64, P]
     L.glm53_sparse_mla_partials_bytes.restype = I64
     L.glm53_sparse_mla_partials_bytes.argtypes = [I64, I64, I64]

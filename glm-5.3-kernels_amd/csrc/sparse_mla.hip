@@ -73,14 +73,18 @@ struct MlaArgs {
   int partials_only;   // write part/lse even for a single split
   int out_align16;     // out rows 16-byte aligned (else 8-byte stores)
   // Paged indices (sparse_mla_kernel<true>): idx holds request-relative
-  // token positions, mapped to flat cache rows by to_flat_row.
+  // token positions, mapped by to_page_unit to the row's 16-byte unit in a
+  // paged cache (kv = page 0, pages page_units units apart, rows row_units
+  // units apart within a page).
   const int32_t* req_id;   // [T] request of each query token
   const int32_t* bt;       // block table, row r at bt + r * bt_stride
   int64_t bt_stride;
   int max_blocks;          // entries per block-table row
   int num_reqs;            // block-table rows: other request ids map to -1
   int block_size;          // tokens per cache block
-  int page_rows;           // rows per physical page in the flat row view
+  int num_blocks;          // physical pages: other table entries map to -1
+  int page_units;          // page stride / 16
+  int row_units;           // row stride / 16
 };
 
 __device__ __forceinline__ float f4_get(const float4& v, int i) {
@@ -158,6 +162,20 @@ __device__ __forceinline__ int to_flat_row(const int32_t* bt_req, int max_blocks
                           static_cast<uint32_t>(off));
 }
 
+// The fused gather's form of the same mapping: the 16-byte unit of the
+// row in the paged cache, or -1 (also for a table entry that is not one of
+// the num_blocks pages, which the flat-row form leaves to the attention's
+// row mask).  The host keeps num_blocks * page_units below 2^31.
+__device__ __forceinline__ int to_page_unit(const int32_t* bt_req, int max_blocks, int block_size,
+                                            int num_blocks, int page_units, int row_units, int pos) {
+  if (pos < 0) return -1;
+  const int blk = pos / block_size;
+  if (blk >= max_blocks) return -1;
+  const int phys = bt_req[blk];
+  if (phys < 0 || phys >= num_blocks) return -1;
+  return phys * page_units + (pos - blk * block_size) * row_units;
+}
+
 template <bool kPaged>
 __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   __shared__ MlaShared sh;
@@ -214,8 +232,10 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
     for (int r = 0; r < kRounds; r++) {
       const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
       int v = pos < end ? idx_t[pos] : -1;
-      if (kPaged) v = to_flat_row(bt_req, max_blocks, a.block_size, a.page_rows, v);
-      if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv) v = -1;
+      if (kPaged)
+        v = to_page_unit(bt_req, max_blocks, a.block_size, a.num_blocks, a.page_units, a.row_units, v);
+      else if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv)
+        v = -1;
       id[r] = v;
     }
     uint4 kd[kRounds][2][2];
@@ -230,14 +250,15 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         kd[r][u][1] = make_uint4(0, 0, 0, 0);
         if (kid >= 0) {
           const uint4* rp = reinterpret_cast<const uint4*>(
-              a.kv + static_cast<int64_t>(kid) * a.skv + kSlice * sl + 32 * g);
+              a.kv + static_cast<int64_t>(kid) * (kPaged ? 16 : a.skv) + kSlice * sl + 32 * g);
           kd[r][u][0] = rp[0];
           kd[r][u][1] = rp[1];
         }
       }
       sv[r] = 0.f;
       if (sl == 0 && lane < kTile && id[r] >= 0)
-        sv[r] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(id[r]) * a.skv + kLatent);
+        sv[r] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(id[r]) * (kPaged ? 16 : a.skv) +
+                                                kLatent);
       vmask[r] = static_cast<uint32_t>(__ballot(id[r] >= 0));
     }
     if (sl == 0 && lane < kTile) {
@@ -590,7 +611,9 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
   a.max_blocks = 0;
   a.num_reqs = 0;
   a.block_size = 1;
-  a.page_rows = 1;
+  a.num_blocks = 0;
+  a.page_units = 0;
+  a.row_units = 0;
   a.so_t = a.so_h = 0;
   return 0;
 }
@@ -686,30 +709,37 @@ extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const
                        so_h, stream);
 }
 
-extern "C" int glm53_sparse_mla_paged(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
-                                      int64_t skv_t, int64_t seq_kv, const int32_t* req_indices,
-                                      int64_t si_t, const int32_t* req_id,
-                                      const int32_t* block_table, int64_t num_reqs,
-                                      int64_t bt_stride, int64_t max_blocks, int64_t block_size,
-                                      int64_t page_rows,
-                                      int64_t num_tokens, int64_t num_heads, int64_t topk,
-                                      double sm_scale, int64_t num_splits, void* workspace,
-                                      int64_t workspace_bytes, void* out, int64_t so_t,
-                                      int64_t so_h, void* stream) {
+extern "C" int glm53_sparse_mla_paged(const void* q, int64_t sq_t, int64_t sq_h, const void* kv_pages,
+                                      int64_t page_bytes, int64_t row_bytes, int64_t num_blocks,
+                                      const int32_t* req_indices, int64_t si_t,
+                                      const int32_t* req_id, const int32_t* block_table,
+                                      int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
+                                      int64_t block_size, int64_t num_tokens, int64_t num_heads,
+                                      int64_t topk, double sm_scale, int64_t num_splits,
+                                      void* workspace, int64_t workspace_bytes, void* out,
+                                      int64_t so_t, int64_t so_h, void* stream) {
+  if (num_blocks < 0 || row_bytes < 528 || page_bytes < 0 || page_bytes % 16 || row_bytes % 16)
+    return num_blocks < 0 || row_bytes < 528 || page_bytes < 0 ? GLM53_ERR_BAD_SHAPE : GLM53_ERR_MISALIGNED;
   MlaArgs a;
-  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, req_indices, si_t, num_tokens, num_heads,
-                   topk, sm_scale, num_splits);
+  int rc = prepare(a, q, sq_t, sq_h, kv_pages, row_bytes, num_blocks, req_indices, si_t, num_tokens,
+                   num_heads, topk, sm_scale, num_splits);
   if (rc) return rc;
   if (num_tokens == 0) return 0;
-  rc = check_paged(req_id, block_table, num_reqs, bt_stride, max_blocks, block_size, page_rows);
+  rc = check_paged(req_id, block_table, num_reqs, bt_stride, max_blocks, block_size, block_size);
   if (rc) return rc;
+  // Rows of a page must fit in it, and every row's 16-byte unit index in an int.
+  if (num_blocks > 0 && (page_bytes < (block_size - 1) * row_bytes + 528 ||
+                         (num_blocks * page_bytes) / 16 > 0x7fffffff))
+    return GLM53_ERR_BAD_SHAPE;
   a.req_id = req_id;
+  a.bt = block_table ? block_table : req_id;   // num_reqs == 0: never read
   a.num_reqs = block_table ? static_cast<int>(num_reqs) : 0;
-  a.bt = block_table ? block_table : req_id;   // max_blocks == 0: never read
   a.bt_stride = bt_stride;
   a.max_blocks = static_cast<int>(max_blocks);
   a.block_size = static_cast<int>(block_size);
-  a.page_rows = static_cast<int>(page_rows);
+  a.num_blocks = static_cast<int>(num_blocks);
+  a.page_units = static_cast<int>(page_bytes / 16);
+  a.row_units = static_cast<int>(row_bytes / 16);
   return run_attention(a, num_tokens, num_heads, num_splits, workspace, workspace_bytes, out, so_t,
                        so_h, stream);
 }

@@ -33,7 +33,6 @@ namespace glm53 {
 namespace {
 
 constexpr int kLatent = 512;
-constexpr int kRowBytes = 528;
 constexpr int kWavesPerBlock = 4;
 constexpr float kRoundMagic = 12582912.0f;  // 1.5 * 2^23
 

@@ -178,20 +178,22 @@ def triton_mla_sparse_attention_paged(
     request-relative indices are mapped to cache rows as
     sparse_utils.triton_convert_req_index_to_global_index maps them, inside
     the attention's index load.  Same result as converting first and calling
-    triton_mla_sparse_attention on sparse_utils.flat_kv_row_view(kv_cache).
+    triton_mla_sparse_attention on sparse_utils.flat_kv_row_view(kv_cache)
+    whenever that view exists; the page stride here may be any multiple of
+    16 bytes (pages padded to an alignment), which the flat view cannot
+    express.
 
     Args:
         q:            [T, H, 512] bf16
-        kv_cache:     int8 [num_blocks, block_size, 528] paged cache (rows
-                      contiguous; the page stride may be padded by whole rows)
+        kv_cache:     int8 [num_blocks, block_size, 528] paged cache (row and
+                      page strides multiples of 16 bytes)
         req_indices:  int32 [T, topk] or [T, 1, topk] request-relative token
                       positions, -1 for padding
         req_id_per_token: int32 [T]
         block_table:  int32 [num_reqs, max_blocks]
     """
-    from sparse_utils import flat_kv_row_view
     assert kv_cache.dtype == torch.int8 and kv_cache.dim() == 3 and kv_cache.shape[2] == _ROW_BYTES
-    rows, page_rows = flat_kv_row_view(kv_cache, kv_cache.shape[1])
+    assert kv_cache.stride(2) == 1
     if req_indices.dim() == 3:
         assert req_indices.shape[1] == 1
         req_indices = req_indices[:, 0, :]
@@ -228,12 +230,12 @@ def triton_mla_sparse_attention_paged(
     with torch.cuda.device(q.device):
         rc = L.glm53_sparse_mla_paged(
             q.data_ptr(), q.stride(0), q.stride(1),
-            rows.data_ptr(), rows.stride(0), rows.shape[0],
+            kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), kv_cache.shape[0],
             req_indices.data_ptr(), req_indices.stride(0),
             req_id_per_token.data_ptr(),
             block_table.data_ptr() if block_table.numel() else None,
             block_table.shape[0], block_table.stride(0), block_table.shape[1],
-            kv_cache.shape[1], page_rows,
+            kv_cache.shape[1],
             num_tokens, num_heads_q, index_topk,
             float(sm_scale), num_kv_splits,
             workspace.data_ptr() if workspace is not None else None, ws_bytes,

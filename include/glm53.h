@@ -98,26 +98,35 @@ int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h,
  *             + p % block_size   (32-bit wrapping arithmetic)
  * page_rows (>= block_size) is the row count of one physical page in the
  * flat row view (vLLM's BLOCK_STRIDE_ROWS; block_size for unpadded pages).
- *
  * glm53_convert_req_index writes the mapped rows (int32 [num_tokens, topk],
  * row stride so_t) -- the conversion alone.
- * glm53_sparse_mla_paged is glm53_sparse_mla with the mapping applied to
- * each index as it is loaded (one launch fewer per decode step; results
- * identical to converting first).  kv / skv_t / seq_kv describe the flat row
- * view (seq_kv = physical pages * page_rows); rows outside [0, seq_kv) are
- * masked as in glm53_sparse_mla.
  */
 int glm53_convert_req_index(const int32_t* req_id, const int32_t* block_table,
                             int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
                             const int32_t* indices, int64_t si_t, int32_t* out,
                             int64_t so_t, int64_t num_tokens, int64_t topk,
                             int64_t block_size, int64_t page_rows, void* stream);
+
+/*
+ * glm53_sparse_mla with request-relative indices resolved inside the
+ * attention's index load (one launch fewer per decode step than converting
+ * first; the same output whenever the flat row view exists).  The cache is
+ * paged: kv_pages is page 0, physical page b starts b * page_bytes bytes
+ * later and holds block_size rows row_bytes apart (page_bytes and row_bytes
+ * multiples of 16, row_bytes >= 528; the page stride may be padded to any
+ * alignment, it need not be a whole number of rows).  Position p of token t
+ * reads row p % block_size of page block_table[req_id[t], p / block_size];
+ * it is masked when p < 0, the request id or block is outside the table, or
+ * the table entry is not in [0, num_blocks).  num_blocks * page_bytes must
+ * stay below 32 GiB.
+ */
 int glm53_sparse_mla_paged(const void* q, int64_t sq_t, int64_t sq_h,
-                           const void* kv, int64_t skv_t, int64_t seq_kv,
+                           const void* kv_pages, int64_t page_bytes, int64_t row_bytes,
+                           int64_t num_blocks,
                            const int32_t* req_indices, int64_t si_t,
                            const int32_t* req_id, const int32_t* block_table,
                            int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
-                           int64_t block_size, int64_t page_rows,
+                           int64_t block_size,
                            int64_t num_tokens, int64_t num_heads, int64_t topk,
                            double sm_scale, int64_t num_splits,
                            void* workspace, int64_t workspace_bytes,

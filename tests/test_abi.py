@@ -143,13 +143,17 @@ def test_paged_entry_points_host_errors():
     assert L.glm53_convert_req_index(fake, fake, 2, 8, 8, fake, 64, fake, 64, 1, 64, 16, 15, None) == -2
     assert L.glm53_convert_req_index(fake, fake, 2, 8, 8, fake, 64, fake, 64, 0, 64, 16, 16, None) == 0
     # paged attention: argument errors before any launch
-    args = [fake, 8192, 512, fake, 528, 1024, fake, 2176, fake, fake, 2, 8, 8, 64, 64,
+    args = [fake, 8192, 512, fake, 36864, 528, 64, fake, 2176, fake, fake, 2, 8, 8, 64,
             1, 16, 2176, 0.04, 4, None, 0, fake, 8192, 512, None]
     assert L.glm53_sparse_mla_paged(*args) == -4                        # no workspace
-    bad = list(args); bad[8] = None
+    bad = list(args); bad[9] = None
     assert L.glm53_sparse_mla_paged(*bad) == -1                         # null req_id
-    bad = list(args); bad[13] = 0
+    bad = list(args); bad[14] = 0
     assert L.glm53_sparse_mla_paged(*bad) == -2                         # block size 0
+    bad = list(args); bad[4] = 36864 + 8
+    assert L.glm53_sparse_mla_paged(*bad) == -3                         # page stride not 16-byte aligned
+    bad = list(args); bad[4] = 63 * 528
+    assert L.glm53_sparse_mla_paged(*bad) == -2                         # 64 rows do not fit the page
     bad = list(args); bad[15] = 0
     assert L.glm53_sparse_mla_paged(*bad) == 0                          # T = 0
 

@@ -19,22 +19,19 @@ MAX_ABS = 2e-2
 MEAN_ABS = 2e-3
 
 
-def paged_cache(cuda, num_blocks, block_size, page_rows, seed):
-    """int8 [num_blocks, block_size, 528] view of pages of page_rows rows,
-    filled by store_int8 through its slot mapping; returns the view and the
-    flat rows as numpy (padding rows included)."""
+def paged_cache(cuda, num_blocks, block_size, page_bytes, seed):
+    """int8 [num_blocks, block_size, 528] cache whose pages start page_bytes
+    apart (padding untouched), filled by store_int8 through its slot mapping;
+    returns the cache and its rows as numpy [num_blocks, block_size, 528]."""
     from titan_kv import store_int8
-    from sparse_utils import flat_kv_row_view
     g = W.gen(cuda, seed)
-    raw = torch.zeros(num_blocks, page_rows, 528, dtype=torch.int8, device=cuda)
-    cache = raw[:, :block_size, :]
+    raw = torch.zeros(num_blocks * page_bytes, dtype=torch.int8, device=cuda)
+    cache = torch.as_strided(raw, (num_blocks, block_size, 528), (page_bytes, 528, 1))
     n = num_blocks * block_size
     x = torch.randn(n, 512, generator=g, device=cuda).to(torch.bfloat16)
     store_int8(x, cache, torch.arange(n, device=cuda))
     torch.cuda.synchronize()
-    rows, stride = flat_kv_row_view(cache, block_size)
-    assert stride == page_rows
-    return cache, rows, rows.contiguous().view(torch.uint8).cpu().numpy()
+    return cache, cache.contiguous().view(torch.uint8).cpu().numpy()
 
 
 def tables(cuda, num_reqs, max_blocks, num_blocks, seed):
@@ -66,16 +63,34 @@ def test_convert_matches_oracle(cuda, oracle, block_size, page_rows, max_blocks,
     assert np.array_equal(out.cpu().numpy(), want)
 
 
+def logical_attention(q, cache, idx, req, bt, splits, sm_scale):
+    """Reference on the GPU: per token, its request's pages copied in
+    block-table order into one contiguous cache, indexed by the raw
+    positions, through the flat-index attention."""
+    from titan_mla import triton_mla_sparse_attention
+    outs = []
+    for t in range(q.shape[0]):
+        pages = cache[bt[int(req[t])].long()]                       # [max_blocks, block_size, 528]
+        flat = pages.reshape(-1, 1, 528).contiguous()
+        outs.append(triton_mla_sparse_attention(q[t:t + 1], flat, idx[t:t + 1].view(1, 1, -1), sm_scale,
+                                                num_kv_splits=splits))
+    return torch.cat(outs)
+
+
 @pytest.mark.parametrize("splits", [1, 8, None])
-@pytest.mark.parametrize("block_size,page_rows", [(64, 64), (64, 66), (2304, 2304)])
-def test_paged_attention_equals_convert_then_attend(cuda, oracle, splits, block_size, page_rows):
-    from sparse_utils import triton_convert_req_index_to_global_index as conv
+@pytest.mark.parametrize("block_size,page_bytes", [(64, 64 * 528), (64, 66 * 528), (64, 36864), (2304, 2304 * 528)])
+def test_paged_attention(cuda, oracle, splits, block_size, page_bytes):
+    """Fused paged attention = per-token attention over the logically ordered
+    cache (bit for bit), = convert + attend on the flat row view when the page
+    stride is a whole number of rows (bit for bit), and within the attention
+    bar of the oracle.  36864 bytes = 64 rows padded to a 4 KB multiple."""
+    from sparse_utils import flat_kv_row_view, triton_convert_req_index_to_global_index as conv
     from titan_mla import triton_mla_sparse_attention, triton_mla_sparse_attention_paged
     from oracle import bf16_to_f32
     max_blocks = 4 if block_size == 2304 else 40
     num_blocks = 3 * max_blocks + 2
-    log_case("paged attention", block_size, page_rows, splits)
-    cache, rows, rows_np = paged_cache(cuda, num_blocks, block_size, page_rows, seed=31)
+    log_case("paged attention", block_size, page_bytes, splits)
+    cache, pages_np = paged_cache(cuda, num_blocks, block_size, page_bytes, seed=31)
     bt = tables(cuda, 3, max_blocks, num_blocks, 7)
     g = W.gen(cuda, 32)
     T, topk = 6, 2176
@@ -84,28 +99,57 @@ def test_paged_attention_equals_convert_then_attend(cuda, oracle, splits, block_
     idx = torch.randint(0, max_blocks * block_size, (T, topk), generator=g, device=cuda, dtype=torch.int32)
     idx[1, -200:] = -1
     idx[2, :50] = max_blocks * block_size + 17          # beyond the table -> masked
+    if splits is None:   # the auto policy for this batch, pinned for the per-token references
+        from titan_mla import _choose_num_kv_splits_mi355x
+        splits = _choose_num_kv_splits_mi355x(T, 1, topk, torch.cuda.get_device_properties(0).multi_processor_count)
     fused = triton_mla_sparse_attention_paged(q, cache, idx, req, bt, W.SM_SCALE, num_kv_splits=splits)
-    flat_idx = conv(req, bt, idx, BLOCK_SIZE=block_size, NUM_TOPK_TOKENS=topk, BLOCK_STRIDE_ROWS=page_rows)
-    two = triton_mla_sparse_attention(q, rows.view(-1, 1, 528), flat_idx.view(T, 1, topk), W.SM_SCALE,
-                                      num_kv_splits=splits)
+    logical = logical_attention(q, cache, torch.where(idx < max_blocks * block_size, idx, -1), req, bt, splits,
+                                W.SM_SCALE)
     torch.cuda.synchronize()
-    assert torch.equal(fused, two)
+    assert torch.equal(fused, logical)
+    if page_bytes % 528 == 0:
+        rows, stride = flat_kv_row_view(cache, block_size)
+        flat_idx = conv(req, bt, idx, BLOCK_SIZE=block_size, NUM_TOPK_TOKENS=topk, BLOCK_STRIDE_ROWS=stride)
+        two = triton_mla_sparse_attention(q, rows.view(-1, 1, 528), flat_idx.view(T, 1, topk), W.SM_SCALE,
+                                          num_kv_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, two)
     # against the oracle over each request's logically ordered cache
     btn, reqn, idxn = bt.cpu().numpy(), req.cpu().numpy(), idx.cpu().numpy()
     qn = q.view(torch.int16).cpu().numpy().view(np.uint16)
     got = fused.float().cpu().numpy()
     for t in range(T):
-        logical = np.concatenate([rows_np[b * page_rows: b * page_rows + block_size] for b in btn[reqn[t]]])
-        li = np.where((idxn[t] >= 0) & (idxn[t] < logical.shape[0]), idxn[t], -1)[None, :]
-        want = bf16_to_f32(oracle.sparse_mla(qn[t:t + 1], logical, li, W.SM_SCALE, n_splits=1))[0]
+        lc = pages_np[btn[reqn[t]]].reshape(-1, 528)
+        li = np.where((idxn[t] >= 0) & (idxn[t] < lc.shape[0]), idxn[t], -1)[None, :]
+        want = bf16_to_f32(oracle.sparse_mla(qn[t:t + 1], lc, li, W.SM_SCALE, n_splits=1))[0]
         err = np.abs(got[t] - want)
         ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
         assert np.all(err <= np.maximum(MAX_ABS, ulp)) and err.mean() <= MEAN_ABS, (t, err.max())
 
 
+def test_paged_table_entries_outside_the_cache_are_masked(cuda):
+    """A block-table entry that is not one of the cache's pages (negative or
+    too large, e.g. a stale or unused slot) masks its positions."""
+    from titan_mla import triton_mla_sparse_attention_paged
+    cache, _ = paged_cache(cuda, 8, 64, 36864, seed=51)
+    g = W.gen(cuda, 52)
+    q = torch.randn(2, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+    bt = torch.tensor([[3, -1, 1, 8], [2, 5, 100000, 0]], dtype=torch.int32, device=cuda)
+    req = torch.tensor([0, 1], dtype=torch.int32, device=cuda)
+    idx = torch.randint(0, 4 * 64, (2, 2176), generator=g, device=cuda, dtype=torch.int32)
+    log_case("paged bad table entries")
+    out = triton_mla_sparse_attention_paged(q, cache, idx, req, bt, W.SM_SCALE, num_kv_splits=4)
+    bad = ((idx // 64 == 1) | (idx // 64 == 3)) & (req[:, None] == 0) | (idx // 64 == 2) & (req[:, None] == 1)
+    clean = torch.where(bad, torch.full_like(idx, -1), idx)
+    good_bt = torch.where(bt < 0, 0, torch.where(bt >= 8, 0, bt))
+    ref = triton_mla_sparse_attention_paged(q, cache, clean, req, good_bt, W.SM_SCALE, num_kv_splits=4)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
 def test_paged_attention_graph_and_bad_requests(cuda):
     from titan_mla import triton_mla_sparse_attention_paged
-    cache, rows, _ = paged_cache(cuda, 40, 64, 66, seed=41)
+    cache, _ = paged_cache(cuda, 40, 64, 66 * 528, seed=41)
     bt = tables(cuda, 2, 16, 40, 9)
     g = W.gen(cuda, 42)
     q = torch.randn(3, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
