@@ -265,10 +265,36 @@ def main():
             gp1.replay()
         us_two = timer.replay_loop(gp2, K // args.unroll) / args.unroll
         us_one = timer.replay_loop(gp1, K // args.unroll) / args.unroll
+        # Indexer output (top-512 pools of 4 tokens + tail): expansion +
+        # conversion + attention, against the one pooled call.
+        from sparse_utils import expand_pools_and_append_tail
+        from titan_mla import triton_mla_sparse_attention_pooled
+        pools_pg, lens_pg = W.pooled_b8_inputs(dev, g8)
+        buf_pg = torch.full((8, 2176), -1, dtype=torch.int32, device=dev)
+
+        def pooled_three():
+            exp = expand_pools_and_append_tail(pools_pg, lens_pg, 4)
+            buf_pg[:, : exp.shape[1]].copy_(exp)
+            flat = triton_convert_req_index_to_global_index(
+                reqpg, btpg, buf_pg, BLOCK_SIZE=pages.shape[1], BLOCK_STRIDE_ROWS=stride_pg, NUM_TOPK_TOKENS=2176)
+            return triton_mla_sparse_attention(qpg, kv_pg, flat.view(8, 1, -1), W.SM_SCALE,
+                                               num_kv_splits=args.splits)
+
+        pooled_one = lambda: triton_mla_sparse_attention_pooled(qpg, pages, pools_pg, lens_pg, 4, reqpg, btpg,
+                                                                W.SM_SCALE, num_kv_splits=args.splits)
+        gq3, _ = capture(torch, pooled_three, args.unroll)
+        gq1, _ = capture(torch, pooled_one, args.unroll)
+        for _ in range(Wm):
+            gq3.replay()
+            gq1.replay()
+        us_q3 = timer.replay_loop(gq3, K // args.unroll) / args.unroll
+        us_q1 = timer.replay_loop(gq1, K // args.unroll) / args.unroll
         extra["decode_b8_paged"] = {"us_per_step_fused": round(us_one, 3),
                                     "us_per_step_convert_then_attend": round(us_two, 3),
+                                    "us_per_step_pooled_fused": round(us_q1, 3),
+                                    "us_per_step_expand_convert_attend": round(us_q3, 3),
                                     "block_size": pages.shape[1], "context_per_request": 32768}
-        del gp1, gp2
+        del gp1, gp2, gq1, gq3
 
         # ------------------------------------------------------------ MoE align
         moe = {}

@@ -20,6 +20,8 @@ EXPORTED = (
     "glm53_sparse_mla",
     "glm53_convert_req_index",
     "glm53_sparse_mla_paged",
+    "glm53_expand_pools",
+    "glm53_sparse_mla_pooled",
     "glm53_sparse_mla_partials_bytes",
     "glm53_sparse_mla_partials",
     "glm53_sparse_mla_merge",
@@ -56,6 +58,11 @@ def load():
     L.glm53_sparse_mla_paged.restype = I
     L.glm53_sparse_mla_paged.argtypes = [P, I64, I64, P, I64, I64, I64, P, I64, P, P, I64, I64, I64, I64,
                                          I64, I64, I64, D, I64, P, I64, P, I64, I64, P]
+    L.glm53_expand_pools.restype = I
+    L.glm53_expand_pools.argtypes = [P, I, I64, I64, P, I64, P, I64, I64, I64, P]
+    L.glm53_sparse_mla_pooled.restype = I
+    L.glm53_sparse_mla_pooled.argtypes = [P, I64, I64, P, I64, I64, I64, P, I64, I64, P, I64, P, P, I64, I64,
+                                          I64, I64, I64, I64, I64, D, I64, P, I64, P, I64, I64, P]
     L.glm53_sparse_mla_partials_bytes.restype = I64
     L.glm53_sparse_mla_partials_bytes.argtypes = [I64, I64, I64]
     L.glm53_sparse_mla_partials.restype = I

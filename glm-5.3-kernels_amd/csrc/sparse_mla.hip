@@ -85,6 +85,13 @@ struct MlaArgs {
   int num_blocks;          // physical pages: other table entries map to -1
   int page_units;          // page stride / 16
   int row_units;           // row stride / 16
+  // Pooled positions (kPooledPos): slot k of token t comes from
+  // pooled_position(pools + t * sp_t, num_pools, pool_size, seq_lens[t], k).
+  const int32_t* pools;
+  int64_t sp_t;
+  int num_pools;
+  int pool_size;
+  const int32_t* seq_lens; // nullptr: no tail slots
 };
 
 __device__ __forceinline__ float f4_get(const float4& v, int i) {
@@ -176,8 +183,35 @@ __device__ __forceinline__ int to_page_unit(const int32_t* bt_req, int max_block
   return phys * page_units + (pos - blk * block_size) * row_units;
 }
 
-template <bool kPaged>
+// Index modes of the attention kernel.
+constexpr int kFlatRows = 0;   // indices are rows of a flat cache
+constexpr int kPagedPos = 1;   // request-relative positions into a paged cache
+constexpr int kPooledPos = 2;  // positions expanded from top-k pool ids, then paged
+
+// Token position held by slot k of a row expanded from pool ids, as the
+// indexer's kpool expansion lays it out (model: tests/verify_indexer_sharding.py:
+// 72-79): slot k < num_pools * pool_size is token pool[k / pool_size] *
+// pool_size + k % pool_size (-1 for a negative pool id); the next
+// pool_size - 1 slots, when seq_len >= 0, are the tail tokens
+// seq_len / pool_size * pool_size + j for j < seq_len % pool_size (-1
+// otherwise); later slots are -1.
+// pool(j) returns pool id j as an int (-1 for an invalid id).
+template <class PoolAt>
+__device__ __forceinline__ int pooled_position(PoolAt pool, int num_pools, int pool_size, int seq_len,
+                                               int k) {
+  const int expanded = num_pools * pool_size;
+  if (k < expanded) {
+    const int pid = pool(k / pool_size);
+    return pid >= 0 ? pid * pool_size + k % pool_size : -1;
+  }
+  const int j = k - expanded;
+  if (seq_len < 0 || j >= pool_size - 1) return -1;
+  return j < seq_len % pool_size ? seq_len / pool_size * pool_size + j : -1;
+}
+
+template <int kMode>
 __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
+  constexpr bool kPaged = kMode != kFlatRows;
   __shared__ MlaShared sh;
 
   const int split = blockIdx.x;
@@ -199,6 +233,8 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   const bool req_ok = req >= 0 && req < a.num_reqs;
   const int32_t* bt_req = kPaged && req_ok ? a.bt + static_cast<int64_t>(req) * a.bt_stride : a.bt;
   const int max_blocks = req_ok ? a.max_blocks : 0;
+  const int32_t* pools_t = kMode == kPooledPos ? a.pools + t * a.sp_t : nullptr;
+  const int seq_len_t = kMode == kPooledPos && a.seq_lens ? a.seq_lens[t] : -1;
 
   // Q^T fragment (B operand of S^T = K Q^T): head c, latents
   // [128 sl + 32g, +32) -> four K-steps of 8.
@@ -231,7 +267,13 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
       const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
-      int v = pos < end ? idx_t[pos] : -1;
+      int v;
+      if (kMode == kPooledPos)
+        v = pos < end ? pooled_position([&](int j) { return pools_t[j]; }, a.num_pools, a.pool_size,
+                                        seq_len_t, pos)
+                      : -1;
+      else
+        v = pos < end ? idx_t[pos] : -1;
       if (kPaged)
         v = to_page_unit(bt_req, max_blocks, a.block_size, a.num_blocks, a.page_units, a.row_units, v);
       else if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv)
@@ -460,6 +502,27 @@ __global__ __launch_bounds__(256) void convert_req_index_kernel(const int32_t* _
                                   idx[t * si_t + k]);
 }
 
+// Standalone pool expansion: out[t][k] = pooled_position(pools[t], ...) for
+// k < out_cols.  pools are int32 or int64; an id outside [0, 2^31) is
+// treated as invalid (-1).
+template <typename PoolT>
+__global__ __launch_bounds__(256) void expand_pools_kernel(const PoolT* __restrict__ pools, int64_t sp_t,
+                                                           int num_pools, int pool_size,
+                                                           const int32_t* __restrict__ seq_lens,
+                                                           int32_t* __restrict__ out, int64_t so_t,
+                                                           int out_cols) {
+  const int t = blockIdx.y;
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  if (k >= out_cols) return;
+  const PoolT* src = pools + t * sp_t;
+  const int seq_len = seq_lens ? seq_lens[t] : -1;
+  auto pool = [&](int j) {
+    const int64_t v = static_cast<int64_t>(src[j]);
+    return v >= 0 && v <= 0x7fffffff ? static_cast<int>(v) : -1;
+  };
+  out[t * so_t + k] = pooled_position(pool, num_pools, pool_size, seq_len, k);
+}
+
 // N-way LSE merge (kernels/titan_mla.py:403-429).  One workgroup per
 // (token, head, 128-latent quarter); 256 threads = 8 split lanes x 32 chunks
 // of 4 latents.  Split lane k handles splits k, k + 8, ...: it loads their
@@ -614,6 +677,11 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
   a.num_blocks = 0;
   a.page_units = 0;
   a.row_units = 0;
+  a.pools = nullptr;
+  a.sp_t = 0;
+  a.num_pools = 0;
+  a.pool_size = 1;
+  a.seq_lens = nullptr;
   a.so_t = a.so_h = 0;
   return 0;
 }
@@ -621,10 +689,12 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
 void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
                   static_cast<unsigned>(a.heads_padded / kHeads));
-  if (a.bt != nullptr)
-    hipLaunchKernelGGL(sparse_mla_kernel<true>, grid, dim3(kThreads), 0, st, a);
+  if (a.pools != nullptr)
+    hipLaunchKernelGGL(sparse_mla_kernel<kPooledPos>, grid, dim3(kThreads), 0, st, a);
+  else if (a.bt != nullptr)
+    hipLaunchKernelGGL(sparse_mla_kernel<kPagedPos>, grid, dim3(kThreads), 0, st, a);
   else
-    hipLaunchKernelGGL(sparse_mla_kernel<false>, grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(sparse_mla_kernel<kFlatRows>, grid, dim3(kThreads), 0, st, a);
 }
 
 void launch_merge(const float* part, const float* lse, int64_t num_tokens, int num_splits,
@@ -764,6 +834,74 @@ extern "C" int glm53_convert_req_index(const int32_t* req_id, const int32_t* blo
                      block_table ? static_cast<int>(num_reqs) : 0, indices, si_t, out, so_t, static_cast<int>(topk), static_cast<int>(block_size),
                      static_cast<int>(page_rows));
   return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int glm53_expand_pools(const void* pool_ids, int ids_is_i64, int64_t sp_t,
+                                  int64_t num_pools, const int32_t* seq_lens, int64_t pool_size,
+                                  int32_t* out, int64_t so_t, int64_t num_rows, int64_t out_cols,
+                                  void* stream) {
+  if (num_rows < 0 || num_pools < 0 || out_cols < 0 || pool_size < 1 || num_rows > 65535 ||
+      num_pools * pool_size + pool_size > 0x7fffffff || out_cols > 0x7fffffff)
+    return GLM53_ERR_BAD_SHAPE;
+  if (num_rows == 0 || out_cols == 0) return 0;
+  if (!out || (!pool_ids && num_pools > 0)) return GLM53_ERR_NULL_POINTER;
+  const dim3 grid(static_cast<unsigned>((out_cols + 255) / 256), static_cast<unsigned>(num_rows));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  (void)hipGetLastError();
+  if (ids_is_i64)
+    hipLaunchKernelGGL(expand_pools_kernel<int64_t>, grid, dim3(256), 0, st,
+                       static_cast<const int64_t*>(pool_ids), sp_t, static_cast<int>(num_pools),
+                       static_cast<int>(pool_size), seq_lens, out, so_t, static_cast<int>(out_cols));
+  else
+    hipLaunchKernelGGL(expand_pools_kernel<int32_t>, grid, dim3(256), 0, st,
+                       static_cast<const int32_t*>(pool_ids), sp_t, static_cast<int>(num_pools),
+                       static_cast<int>(pool_size), seq_lens, out, so_t, static_cast<int>(out_cols));
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int glm53_sparse_mla_pooled(const void* q, int64_t sq_t, int64_t sq_h, const void* kv_pages,
+                                       int64_t page_bytes, int64_t row_bytes, int64_t num_blocks,
+                                       const int32_t* pool_ids, int64_t sp_t, int64_t num_pools,
+                                       const int32_t* seq_lens, int64_t pool_size,
+                                       const int32_t* req_id, const int32_t* block_table,
+                                       int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
+                                       int64_t block_size, int64_t num_tokens, int64_t num_heads,
+                                       int64_t topk, double sm_scale, int64_t num_splits,
+                                       void* workspace, int64_t workspace_bytes, void* out,
+                                       int64_t so_t, int64_t so_h, void* stream) {
+  if (num_pools < 0 || pool_size < 1 || num_pools * pool_size + pool_size > 0x7fffffff)
+    return GLM53_ERR_BAD_SHAPE;
+  if (num_tokens > 0 && num_pools > 0 && !pool_ids) return GLM53_ERR_NULL_POINTER;
+  if (num_blocks < 0 || row_bytes < 528 || page_bytes < 0 || page_bytes % 16 || row_bytes % 16)
+    return num_blocks < 0 || row_bytes < 528 || page_bytes < 0 ? GLM53_ERR_BAD_SHAPE : GLM53_ERR_MISALIGNED;
+  MlaArgs a;
+  // pool_ids stand in for the index pointer (never read as indices)
+  int rc = prepare(a, q, sq_t, sq_h, kv_pages, row_bytes, num_blocks,
+                   pool_ids ? pool_ids : reinterpret_cast<const int32_t*>(req_id), sp_t, num_tokens,
+                   num_heads, topk, sm_scale, num_splits);
+  if (rc) return rc;
+  if (num_tokens == 0) return 0;
+  rc = check_paged(req_id, block_table, num_reqs, bt_stride, max_blocks, block_size, block_size);
+  if (rc) return rc;
+  if (num_blocks > 0 && (page_bytes < (block_size - 1) * row_bytes + 528 ||
+                         (num_blocks * page_bytes) / 16 > 0x7fffffff))
+    return GLM53_ERR_BAD_SHAPE;
+  a.req_id = req_id;
+  a.bt = block_table ? block_table : req_id;
+  a.num_reqs = block_table ? static_cast<int>(num_reqs) : 0;
+  a.bt_stride = bt_stride;
+  a.max_blocks = static_cast<int>(max_blocks);
+  a.block_size = static_cast<int>(block_size);
+  a.num_blocks = static_cast<int>(num_blocks);
+  a.page_units = static_cast<int>(page_bytes / 16);
+  a.row_units = static_cast<int>(row_bytes / 16);
+  a.pools = pool_ids ? pool_ids : req_id;    // num_pools == 0: never read
+  a.sp_t = sp_t;
+  a.num_pools = static_cast<int>(num_pools);
+  a.pool_size = static_cast<int>(pool_size);
+  a.seq_lens = seq_lens;
+  return run_attention(a, num_tokens, num_heads, num_splits, workspace, workspace_bytes, out, so_t,
+                       so_h, stream);
 }
 
 extern "C" int glm53_sparse_mla_partials(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,

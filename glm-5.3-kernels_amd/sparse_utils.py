@@ -14,6 +14,11 @@ block_table[r, p // BLOCK_SIZE] * BLOCK_STRIDE_ROWS + p % BLOCK_SIZE, and to
 -1 when p < 0 or its block lies beyond the table).  Both run on the GPU;
 titan_mla.triton_mla_sparse_attention_paged fuses the conversion into the
 attention gather.
+
+Also here: the indexer's kpool expansion (expand_pools_and_append_tail,
+expand_pools_to_tokens: top-k pool ids -> token positions), the step before
+the conversion; titan_mla.triton_mla_sparse_attention_pooled fuses both into
+the attention gather.
 """
 import torch
 
@@ -84,3 +89,46 @@ def triton_convert_req_index_to_global_index(
             T, topk, BLOCK_SIZE, stride_rows, _lib.stream_handle(token_indices.device))
     _lib.check(rc, "glm53_convert_req_index")
     return out
+
+
+def _expand(pool_ids: torch.Tensor, seq_lens, pool_size: int, out_cols: int) -> torch.Tensor:
+    assert pool_ids.dim() == 2 and pool_ids.dtype in (torch.int32, torch.int64)
+    if pool_ids.stride(1) != 1:
+        pool_ids = pool_ids.contiguous()
+    rows, num_pools = pool_ids.shape
+    out = torch.empty((rows, out_cols), dtype=torch.int32, device=pool_ids.device)
+    if rows == 0 or out_cols == 0:
+        return out
+    if seq_lens is not None:
+        seq_lens = seq_lens.to(torch.int32).contiguous()
+        assert seq_lens.numel() == rows
+    L = _lib.load()
+    with torch.cuda.device(pool_ids.device):
+        rc = L.glm53_expand_pools(pool_ids.data_ptr(), int(pool_ids.dtype == torch.int64), pool_ids.stride(0),
+                                  num_pools, seq_lens.data_ptr() if seq_lens is not None else None, pool_size,
+                                  out.data_ptr(), out.stride(0), rows, out_cols,
+                                  _lib.stream_handle(pool_ids.device))
+    _lib.check(rc, "glm53_expand_pools")
+    return out
+
+
+def expand_pools_and_append_tail(pool_ids: torch.Tensor, seq_lens: torch.Tensor, pool_size: int) -> torch.Tensor:
+    """The indexer's kpool expansion with the tail pool (the operation the
+    reference's sharding patch calls, integration/patch_indexer_sharding.py:
+    92-94; CPU model tests/verify_indexer_sharding.py:72-79): row t becomes
+    pool_ids[t, j] * pool_size + o for every pool j and offset o (-1 for a
+    negative id), then the pool_size - 1 tail slots seq_lens[t] // pool_size
+    * pool_size + j for j < seq_lens[t] % pool_size (-1 otherwise).
+    Returns int32 [rows, num_pools * pool_size + pool_size - 1]."""
+    return _expand(pool_ids, seq_lens, pool_size, pool_ids.shape[1] * pool_size + pool_size - 1)
+
+
+def expand_pools_to_tokens(pool_ids: torch.Tensor, valid: torch.Tensor, topk_tokens: int,
+                           pool_size: int) -> torch.Tensor:
+    """The expansion without a tail (no positions; patch_indexer_sharding.py:
+    97-99).  Pools where `valid` is False count as -1.  Returns int32
+    [rows, topk_tokens] (topk_tokens = num_pools * pool_size)."""
+    assert topk_tokens == pool_ids.shape[1] * pool_size
+    if valid is not None:
+        pool_ids = torch.where(valid, pool_ids, torch.full_like(pool_ids, -1))
+    return _expand(pool_ids, None, pool_size, topk_tokens)

@@ -245,6 +245,88 @@ def triton_mla_sparse_attention_paged(
     return out
 
 
+def triton_mla_sparse_attention_pooled(
+    q: torch.Tensor,
+    kv_cache: torch.Tensor,
+    pool_ids: torch.Tensor,
+    seq_lens: torch.Tensor | None,
+    pool_size: int,
+    req_id_per_token: torch.Tensor,
+    block_table: torch.Tensor,
+    sm_scale: float,
+    topk: int = 2176,
+    num_kv_splits: int | None = None,
+    sm_count: int | None = None,
+) -> torch.Tensor:
+    """Indexer output straight to attention: slot k of token t's topk index
+    slots is the position sparse_utils.expand_pools_and_append_tail (or
+    expand_pools_to_tokens when seq_lens is None) puts there, -1 past the
+    expansion, and the positions are resolved through the block table as in
+    triton_mla_sparse_attention_paged.  One launch replaces expansion,
+    conversion and the attention's split kernel; the output equals
+    expanding into a -1-filled [T, topk] buffer and calling the paged
+    attention.
+
+    Args:
+        pool_ids:  int32 [T, num_pools] request-relative pool ids (-1 invalid)
+        seq_lens:  int32 [T] query sequence lengths (position + 1), or None
+        topk:      index slots (multiple of 32, >= the expanded width)
+    """
+    assert kv_cache.dtype == torch.int8 and kv_cache.dim() == 3 and kv_cache.shape[2] == _ROW_BYTES
+    assert kv_cache.stride(2) == 1
+    assert pool_ids.dtype == torch.int32 and pool_ids.dim() == 2
+    assert req_id_per_token.dtype == torch.int32 and block_table.dtype == torch.int32 and block_table.dim() == 2
+    num_tokens, num_heads_q, dim_qk = q.shape
+    assert dim_qk == _BLOCK_DMODEL and q.dtype == torch.bfloat16
+    assert pool_ids.shape[0] == num_tokens and req_id_per_token.numel() == num_tokens
+    assert topk % _MIN_BLOCK_N == 0, f"topk ({topk}) must be a multiple of {_MIN_BLOCK_N}"
+    assert pool_size >= 1
+    width = pool_ids.shape[1] * pool_size + (pool_size - 1 if seq_lens is not None else 0)
+    assert topk >= width, f"topk ({topk}) is narrower than the expansion ({width})"
+
+    num_head_groups = triton_cdiv(num_heads_q, min(_BLOCK_H, num_heads_q))
+    if num_kv_splits is None or num_kv_splits == 0:
+        if sm_count is None:
+            sm_count = num_compute_units(q.device.index)
+        num_kv_splits = _choose_num_kv_splits_mi355x(num_tokens, num_head_groups, topk, sm_count)
+    if num_kv_splits < 1:
+        raise ValueError(f"num_kv_splits must be >= 1, got {num_kv_splits}")
+    out = torch.empty((num_tokens, num_heads_q, _BLOCK_DV), dtype=torch.bfloat16, device=q.device)
+    if num_tokens == 0:
+        return out
+    if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    if pool_ids.stride(1) != 1:
+        pool_ids = pool_ids.contiguous()
+    if seq_lens is not None:
+        assert seq_lens.numel() == num_tokens
+        seq_lens = seq_lens.to(torch.int32).contiguous()
+    if block_table.stride(1) != 1:
+        block_table = block_table.contiguous()
+    req_id_per_token = req_id_per_token.contiguous()
+
+    L = _lib.load()
+    ws_bytes = L.glm53_sparse_mla_workspace_bytes(num_tokens, num_heads_q, num_kv_splits)
+    workspace = (torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None)
+    with torch.cuda.device(q.device):
+        rc = L.glm53_sparse_mla_pooled(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            kv_cache.data_ptr(), kv_cache.stride(0), kv_cache.stride(1), kv_cache.shape[0],
+            pool_ids.data_ptr(), pool_ids.stride(0), pool_ids.shape[1],
+            seq_lens.data_ptr() if seq_lens is not None else None, pool_size,
+            req_id_per_token.data_ptr(),
+            block_table.data_ptr() if block_table.numel() else None,
+            block_table.shape[0], block_table.stride(0), block_table.shape[1],
+            kv_cache.shape[1],
+            num_tokens, num_heads_q, topk,
+            float(sm_scale), num_kv_splits,
+            workspace.data_ptr() if workspace is not None else None, ws_bytes,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.stream_handle(q.device))
+    _lib.check(rc, "glm53_sparse_mla_pooled")
+    return out
+
+
 def sparse_mla_partials(q, kv, indices, sm_scale, num_kv_splits):
     """First stage only: per-split normalised outputs and LSEs (fp32) in one
     buffer laid out as glm53.h documents (part [T*S*Hp, 512] then lse

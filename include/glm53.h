@@ -134,6 +134,41 @@ int glm53_sparse_mla_paged(const void* q, int64_t sq_t, int64_t sq_h,
                            void* stream);
 
 /*
+ * Pool expansion, the last step of the sparse indexer: it selects the top-k
+ * pools of pool_size consecutive tokens and expands them to token positions
+ * (model: tests/verify_indexer_sharding.py:72-79).  Row t, slot k:
+ *   k < num_pools * pool_size:  pool_ids[t][k / pool_size] * pool_size
+ *                               + k % pool_size, or -1 for a negative id;
+ *   next pool_size - 1 slots (seq_lens given): the tail tokens
+ *                               seq_lens[t] / pool_size * pool_size + j for
+ *                               j < seq_lens[t] % pool_size, else -1;
+ *   later slots:                -1.
+ * glm53_expand_pools writes slots [0, out_cols) (int32, row stride so_t);
+ * pool ids are int32 or int64 (ids_is_i64), row stride sp_t elements;
+ * seq_lens may be NULL (no tail slots).  glm53_sparse_mla_pooled is
+ * glm53_sparse_mla_paged with each index slot computed this way inside the
+ * attention's index load (int32 pool ids): the indexer's pool ids go
+ * straight to the attention.
+ */
+int glm53_expand_pools(const void* pool_ids, int ids_is_i64, int64_t sp_t,
+                       int64_t num_pools, const int32_t* seq_lens, int64_t pool_size,
+                       int32_t* out, int64_t so_t, int64_t num_rows, int64_t out_cols,
+                       void* stream);
+int glm53_sparse_mla_pooled(const void* q, int64_t sq_t, int64_t sq_h,
+                            const void* kv_pages, int64_t page_bytes, int64_t row_bytes,
+                            int64_t num_blocks,
+                            const int32_t* pool_ids, int64_t sp_t, int64_t num_pools,
+                            const int32_t* seq_lens, int64_t pool_size,
+                            const int32_t* req_id, const int32_t* block_table,
+                            int64_t num_reqs, int64_t bt_stride, int64_t max_blocks,
+                            int64_t block_size,
+                            int64_t num_tokens, int64_t num_heads, int64_t topk,
+                            double sm_scale, int64_t num_splits,
+                            void* workspace, int64_t workspace_bytes,
+                            void* out, int64_t so_t, int64_t so_h,
+                            void* stream);
+
+/*
  * The two stages of glm53_sparse_mla, exposed for callers that merge split
  * results themselves (for example after gathering one token's splits from
  * several devices).  Same stages as the reference's _sparse_mla_kernel_split

@@ -18,6 +18,9 @@ triton_convert_req_index_to_global_index, not available here):
 * convert_req_index     -- parity with vLLM unpinned; pinned by invariants
   (identity table, page/offset decomposition, masking) and by attention over
   the logically gathered cache (tests/test_oracle.py).
+* expand_pools          -- the indexer's kpool expansion, following the
+  reference's CPU model (tests/verify_indexer_sharding.py:72-79); pinned by
+  an independent set formulation and closed-form cases (tests/test_oracle.py).
 
 Pinning (what each function is checked against, in tests/test_oracle.py):
 * store_int8: exact rational arithmetic (fractions.Fraction) on golden rows,
@@ -248,4 +251,29 @@ def convert_req_index(req_id: np.ndarray, block_table: np.ndarray, indices: np.n
         row = base * np.uint32(page_rows) + (p - np.maximum(blk, 0) * block_size).astype(np.uint32)
         out[t] = np.where(ok, row.astype(np.uint32).view(np.int32), -1)
     return out
+
+
+def expand_pools(pool_ids: np.ndarray, seq_lens, pool_size: int, out_cols: int | None = None) -> np.ndarray:
+    """Pool ids [rows, K] -> token positions (tests/verify_indexer_sharding.py:
+    72-79): slot j * pool_size + o holds pool_ids[r, j] * pool_size + o (-1 for
+    a negative id); with seq_lens, the next pool_size - 1 slots hold the tail
+    tokens seq_lens[r] // pool_size * pool_size + o for o < seq_lens[r] %
+    pool_size (-1 otherwise).  Slots up to out_cols past that are -1."""
+    p = np.asarray(pool_ids, dtype=np.int64)
+    rows, k = p.shape
+    width = k * pool_size + (pool_size - 1 if seq_lens is not None else 0)
+    out_cols = width if out_cols is None else out_cols
+    out = np.full((rows, out_cols), -1, dtype=np.int64)
+    offs = np.arange(pool_size)
+    body = np.where(p[:, :, None] >= 0, p[:, :, None] * pool_size + offs[None, None, :], -1).reshape(rows, -1)
+    n = min(out_cols, k * pool_size)
+    out[:, :n] = body[:, :n]
+    if seq_lens is not None:
+        s = np.asarray(seq_lens, dtype=np.int64)
+        tail = np.where(offs[None, : pool_size - 1] < (s % pool_size)[:, None],
+                        (s // pool_size * pool_size)[:, None] + offs[None, : pool_size - 1], -1)
+        lo, hi = k * pool_size, min(out_cols, width)
+        if hi > lo:
+            out[:, lo:hi] = tail[:, : hi - lo]
+    return out.astype(np.int32)
 

@@ -166,3 +166,58 @@ def test_paged_attention_graph_and_bad_requests(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("pool_size,with_tail,dtype", [(4, True, torch.int32), (4, False, torch.int64),
+                                                       (1, True, torch.int32), (5, True, torch.int64)])
+def test_expand_pools_matches_oracle(cuda, oracle, pool_size, with_tail, dtype):
+    from sparse_utils import expand_pools_and_append_tail, expand_pools_to_tokens
+    log_case("expand pools", pool_size, with_tail, dtype)
+    g = W.gen(cuda, 61)
+    rows, k = 7, 512
+    pools = torch.randint(-3, 20000, (rows, k), generator=g, device=cuda).to(dtype)
+    if dtype == torch.int64:
+        pools[0, :5] = 1 << 33                      # not an int32 pool id -> -1
+    lens = torch.randint(0, 90000, (rows,), generator=g, device=cuda, dtype=torch.int32)
+    if with_tail:
+        got = expand_pools_and_append_tail(pools, lens, pool_size)
+        want = oracle.expand_pools(np.where(pools.cpu().numpy() > 2 ** 31 - 1, -1, pools.cpu().numpy()),
+                                   lens.cpu().numpy(), pool_size)
+    else:
+        valid = pools >= 0
+        valid[1, 7] = False
+        got = expand_pools_to_tokens(pools, valid, k * pool_size, pool_size)
+        pn = np.where(valid.cpu().numpy(), pools.cpu().numpy(), -1)
+        want = oracle.expand_pools(np.where(pn > 2 ** 31 - 1, -1, pn), None, pool_size)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape and np.array_equal(got.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("splits", [1, 8, None])
+@pytest.mark.parametrize("with_tail", [True, False])
+def test_pooled_attention_equals_expand_then_paged(cuda, splits, with_tail):
+    """Pool ids straight to attention = expansion into a -1-filled 2176-slot
+    buffer, then the paged attention (bit for bit)."""
+    from sparse_utils import expand_pools_and_append_tail, expand_pools_to_tokens
+    from titan_mla import triton_mla_sparse_attention_paged, triton_mla_sparse_attention_pooled
+    log_case("pooled attention", splits, with_tail)
+    block_size, max_blocks = 64, 40
+    cache, _ = paged_cache(cuda, 3 * max_blocks + 2, block_size, 36864, seed=71)
+    bt = tables(cuda, 3, max_blocks, 3 * max_blocks + 2, 17)
+    g = W.gen(cuda, 72)
+    T, pool_size, k = 5, 4, 512
+    ctx = max_blocks * block_size
+    req = torch.tensor([0, 2, 1, 0, 2], dtype=torch.int32, device=cuda)
+    q = torch.randn(T, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+    pools = torch.randint(-1, ctx // pool_size, (T, k), generator=g, device=cuda, dtype=torch.int32)
+    lens = torch.randint(ctx - 50, ctx, (T,), generator=g, device=cuda, dtype=torch.int32)
+    seq = lens if with_tail else None
+    fused = triton_mla_sparse_attention_pooled(q, cache, pools, seq, pool_size, req, bt, W.SM_SCALE, topk=2176,
+                                               num_kv_splits=splits)
+    exp = (expand_pools_and_append_tail(pools, lens, pool_size) if with_tail
+           else expand_pools_to_tokens(pools, pools >= 0, k * pool_size, pool_size))
+    buf = torch.full((T, 2176), -1, dtype=torch.int32, device=cuda)
+    buf[:, : exp.shape[1]] = exp
+    two = triton_mla_sparse_attention_paged(q, cache, buf, req, bt, W.SM_SCALE, num_kv_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two)

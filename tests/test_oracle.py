@@ -383,3 +383,33 @@ def test_paged_attention_equals_logical_cache(oracle, page_rows):
     bad2 = bf16_to_f32(oracle.sparse_mla(q, flat, oracle.convert_req_index(req, bt, swapped, bs, pr), 512 ** -0.5,
                                          n_splits=2))
     assert not np.array_equal(bad2, via_pages)
+
+
+# ---- kpool expansion (the indexer's last step) ----
+
+def test_expand_pools_closed_forms(oracle):
+    out = oracle.expand_pools(np.array([[2, -1, 0]]), np.array([11]), 4)
+    assert out.tolist() == [[8, 9, 10, 11, -1, -1, -1, -1, 0, 1, 2, 3, 8, 9, 10]]
+    out = oracle.expand_pools(np.array([[5, 1]]), np.array([8]), 4, out_cols=12)
+    assert out.tolist() == [[20, 21, 22, 23, 4, 5, 6, 7, -1, -1, -1, -1]]   # 8 % 4 == 0: empty tail
+    assert oracle.expand_pools(np.array([[3]]), None, 1).tolist() == [[3]]
+    assert oracle.expand_pools(np.array([[7, 2]]), np.array([100]), 1).tolist() == [[7, 2]]  # pool 1: no tail slots
+
+
+def test_expand_pools_set_formulation(oracle):
+    """The multiset of valid positions equals the union of each valid pool's
+    tokens and the tail tokens [len // P * P, len), and every slot's position
+    lies in its own pool (or the tail range)."""
+    rng = np.random.default_rng(8)
+    for P in (1, 2, 4, 5):
+        pools = rng.integers(-2, 300, size=(6, 37))
+        lens = rng.integers(0, 1300, size=6)
+        out = oracle.expand_pools(pools, lens, P, out_cols=37 * P + P - 1 + 9)
+        for r in range(6):
+            want = sorted([int(p) * P + o for p in pools[r] if p >= 0 for o in range(P)] +
+                          list(range(lens[r] // P * P, lens[r])))
+            got = out[r]
+            assert sorted(int(v) for v in got if v >= 0) == want
+            for k, v in enumerate(got[: 37 * P]):
+                assert v == -1 or v // P == pools[r, k // P]
+            assert np.all(got[37 * P + P - 1:] == -1)

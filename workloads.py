@@ -138,6 +138,21 @@ def paged_b8_inputs(device, g, cache, block_size=64, context=32768):
     return pages, q, idx, req, bt
 
 
+def pooled_b8_inputs(device, g, context=32768, pool_size=4, num_pools=512):
+    """Indexer output for the paged B=8 decode: per request, 512 distinct
+    top pools of 4 tokens (half among the last 1024 pools, half anywhere) and
+    the query's sequence length (context - 1: a 3-token tail pool)."""
+    n_pools = context // pool_size
+    rows = []
+    for _ in range(8):
+        recent = n_pools - 1024 + torch.randperm(1024, generator=g, device=device)[: num_pools // 2]
+        rest = torch.randperm(n_pools - 1024, generator=g, device=device)[: num_pools // 2]
+        rows.append(torch.cat([recent, rest])[torch.randperm(num_pools, generator=g, device=device)])
+    pools = torch.stack(rows).to(torch.int32).contiguous()
+    seq_lens = torch.full((8,), context - 1, device=device, dtype=torch.int32)
+    return pools, seq_lens
+
+
 def prefill_inputs(device, g, n_rows=262144, tokens=2048):
     q = torch.randn(tokens, HEADS, LATENT, generator=g, device=device).to(torch.bfloat16)
     pos = n_rows - tokens + torch.arange(tokens, device=device)
