@@ -221,3 +221,23 @@ def test_pooled_attention_equals_expand_then_paged(cuda, splits, with_tail):
     two = triton_mla_sparse_attention_paged(q, cache, buf, req, bt, W.SM_SCALE, num_kv_splits=splits)
     torch.cuda.synchronize()
     assert torch.equal(fused, two)
+
+
+@pytest.mark.parametrize("max_blocks", [8000, 9000])
+def test_paged_long_block_tables(cuda, max_blocks):
+    """Block-table rows up to 8192 entries are staged in LDS, longer ones are
+    read from memory; both give the logical-cache result."""
+    log_case("paged long table", max_blocks)
+    block_size = 1
+    num_blocks = max_blocks + 5
+    cache, _ = paged_cache(cuda, num_blocks, block_size, 528, seed=81)
+    bt = tables(cuda, 1, max_blocks, num_blocks, 19)
+    g = W.gen(cuda, 82)
+    q = torch.randn(2, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+    req = torch.zeros(2, dtype=torch.int32, device=cuda)
+    idx = torch.randint(0, max_blocks, (2, 2176), generator=g, device=cuda, dtype=torch.int32)
+    from titan_mla import triton_mla_sparse_attention_paged
+    fused = triton_mla_sparse_attention_paged(q, cache, idx, req, bt, W.SM_SCALE, num_kv_splits=8)
+    ref = logical_attention(q, cache, idx, req, bt, 8, W.SM_SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ref)
