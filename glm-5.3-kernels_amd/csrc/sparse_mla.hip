@@ -209,7 +209,7 @@ __device__ __forceinline__ int pooled_position(PoolAt pool, int num_pools, int p
   return j < seq_len % pool_size ? seq_len / pool_size * pool_size + j : -1;
 }
 
-template <int kMode>
+template <int kMode, bool kPipe>
 __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   constexpr bool kPaged = kMode != kFlatRows;
   __shared__ MlaShared sh;
@@ -259,11 +259,13 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   float m_run = kNegLarge, l_run = 0.f;
   bool acc_zero = true;  // wave-uniform: no PV product accumulated yet
 
-  int buf = 0, cbuf = 0;
-  for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile, cbuf ^= 1) {
-    // ---- issue every load of the chunk: indices, then rows and scales.
-    // Round r of this key group is chunk tile 2r + kg.
-    int id[kRounds];
+  // kPipe (splits of several chunks): the next chunk's indices are
+  // requested before this chunk's first rounds and its rows after its first
+  // half, so their latency overlaps this chunk's compute.  Without kPipe
+  // (one-chunk decode splits) a chunk's loads are issued at its start.
+  // Index addresses are clamped into the split; positions past it become -1
+  // and load no rows.
+  auto load_ids = [&](int c0, int (&id)[kRounds]) {
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
       const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
@@ -272,22 +274,26 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         v = pos < end ? pooled_position([&](int j) { return pools_t[j]; }, a.num_pools, a.pool_size,
                                         seq_len_t, pos)
                       : -1;
+      else if (kPipe)
+        v = idx_t[min(pos, end - 1)];   // unconditional: the prefetch needs no branch
       else
         v = pos < end ? idx_t[pos] : -1;
+      id[r] = v;
+    }
+  };
+  auto issue_rows = [&](int c0, const int (&raw)[kRounds], uint4 (&kd)[kRounds][2][2], float (&sv)[kRounds],
+                        uint32_t (&vmask)[kRounds]) {
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+      const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
+      int v = pos < end ? raw[r] : -1;
       if (kPaged)
         v = to_page_unit(bt_req, max_blocks, a.block_size, a.num_blocks, a.page_units, a.row_units, v);
       else if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv)
         v = -1;
-      id[r] = v;
-    }
-    uint4 kd[kRounds][2][2];
-    uint32_t vmask[kRounds];
-    float sv[kRounds];
-#pragma unroll
-    for (int r = 0; r < kRounds; r++) {
 #pragma unroll
       for (int u = 0; u < 2; u++) {
-        const int kid = __shfl(id[r], 16 * u + c, 64);
+        const int kid = __shfl(v, 16 * u + c, 64);
         kd[r][u][0] = make_uint4(0, 0, 0, 0);
         kd[r][u][1] = make_uint4(0, 0, 0, 0);
         if (kid >= 0) {
@@ -298,21 +304,42 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         }
       }
       sv[r] = 0.f;
-      if (sl == 0 && lane < kTile && id[r] >= 0)
-        sv[r] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(id[r]) * (kPaged ? 16 : a.skv) +
+      if (sl == 0 && lane < kTile && v >= 0)
+        sv[r] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(v) * (kPaged ? 16 : a.skv) +
                                                 kLatent);
-      vmask[r] = static_cast<uint32_t>(__ballot(id[r] >= 0));
+      vmask[r] = static_cast<uint32_t>(__ballot(v >= 0));
+    }
+  };
+
+  int buf = 0, cbuf = 0;
+  int idc[kRounds], idn[kRounds];
+  uint4 kdc[kRounds][2][2], kdn[kRounds][2][2];
+  float svc[kRounds], svn[kRounds];
+  uint32_t vmc[kRounds], vmn[kRounds];
+  if (kPipe && start < end) {
+    load_ids(start, idc);
+    issue_rows(start, idc, kdc, svc, vmc);
+  }
+  for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile, cbuf ^= 1) {
+    const int c1 = c0 + kChunkTiles * kTile;
+    if (!kPipe) {
+      load_ids(c0, idc);
+      issue_rows(c0, idc, kdc, svc, vmc);
     }
     if (sl == 0 && lane < kTile) {
 #pragma unroll
-      for (int r = 0; r < kRounds; r++) sh.scl[cbuf][2 * r + kg][lane] = sv[r];
+      for (int r = 0; r < kRounds; r++) sh.scl[cbuf][2 * r + kg][lane] = svc[r];
     }
+    if (kPipe) load_ids(c1, idn);
 
     // ---- consume the chunk: one tile per key group per round.
 #pragma unroll
     for (int r = 0; r < kRounds; r++, buf ^= 1) {
-      if (c0 + 2 * r * kTile >= end) break;                      // uniform across the workgroup
+      if (kPipe && r == kRounds / 2) issue_rows(c1, idn, kdn, svn, vmn);   // next chunk's rows (-1 past the split)
+      if (c0 + 2 * r * kTile >= end) continue;                   // uniform across the workgroup
       const bool has_tile = c0 + (2 * r + kg) * kTile < end;     // uniform across the wave
+      uint4 (&kd)[kRounds][2][2] = kdc;
+      uint32_t (&vmask)[kRounds] = vmc;
 
       if (has_tile) {
         f32x4 s_part[2];
@@ -413,6 +440,17 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, acc[dt], 0, 0, 0);
       }
       acc_zero = false;
+    }
+    if (!kPipe) continue;
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+      vmc[r] = vmn[r];
+      svc[r] = svn[r];
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        kdc[r][u][0] = kdn[r][u][0];
+        kdc[r][u][1] = kdn[r][u][1];
+      }
     }
   }
 
@@ -689,12 +727,18 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
 void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
                   static_cast<unsigned>(a.heads_padded / kHeads));
-  if (a.pools != nullptr)
-    hipLaunchKernelGGL(sparse_mla_kernel<kPooledPos>, grid, dim3(kThreads), 0, st, a);
-  else if (a.bt != nullptr)
-    hipLaunchKernelGGL(sparse_mla_kernel<kPagedPos>, grid, dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(sparse_mla_kernel<kFlatRows>, grid, dim3(kThreads), 0, st, a);
+  // Splits longer than one chunk of gathers pipeline their chunks.
+  const bool pipe = a.split_len > kChunkTiles * kTile;
+  const int mode = a.pools != nullptr ? kPooledPos : a.bt != nullptr ? kPagedPos : kFlatRows;
+#define GLM53_LAUNCH(M, P) hipLaunchKernelGGL((sparse_mla_kernel<M, P>), grid, dim3(kThreads), 0, st, a)
+  if (mode == kPooledPos) {
+    if (pipe) GLM53_LAUNCH(kPooledPos, true); else GLM53_LAUNCH(kPooledPos, false);
+  } else if (mode == kPagedPos) {
+    if (pipe) GLM53_LAUNCH(kPagedPos, true); else GLM53_LAUNCH(kPagedPos, false);
+  } else {
+    if (pipe) GLM53_LAUNCH(kFlatRows, true); else GLM53_LAUNCH(kFlatRows, false);
+  }
+#undef GLM53_LAUNCH
 }
 
 void launch_merge(const float* part, const float* lse, int64_t num_tokens, int num_splits,
