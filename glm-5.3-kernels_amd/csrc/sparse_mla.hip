@@ -147,7 +147,7 @@ struct __attribute__((aligned(16))) MlaShared {
       float ml[kGroups][kHeads][2];                    // each key group's (m, l) per head
     } fin;
   };
-  float red[2][kGroups][kSlices][64][8];               // partial S^T per slice
+  float4 red[2][kGroups][kSlices][2][64];              // partial S^T per slice: [half][lane]
   float scl[2][kChunkTiles][kTile];                    // row scales of the chunk
 };
 
@@ -207,6 +207,16 @@ __device__ __forceinline__ int pooled_position(PoolAt pool, int num_pools, int p
   const int j = k - expanded;
   if (seq_len < 0 || j >= pool_size - 1) return -1;
   return j < seq_len % pool_size ? seq_len / pool_size * pool_size + j : -1;
+}
+
+// V slice element (row, col) in LDS.  Rows are 288 bytes (72 dwords) apart,
+// so the four rows of a ds_read_b64_tr_b16 lane group land on distinct
+// banks; the 16-byte chunks of rows 8-15 of every 16 (row bit 3) are XOR-
+// swapped in pairs so that a 16-byte write of 16 consecutive rows at one
+// column is conflict-free too (without it rows r and r + 8 share banks).
+__device__ __forceinline__ uint16_t* vbuf_at(MlaShared& sh, int w, int row, int col) {
+  const int chunk = (col >> 3) ^ ((row >> 3) & 1);
+  return &sh.vbuf[w][row][(chunk << 3) | (col & 7)];
 }
 
 template <int kMode, bool kPipe>
@@ -355,15 +365,14 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
           sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k67, qf[3], sacc, 0, 0, 0);
           s_part[u] = sacc;
           // V slice for the PV product: row 16u + c, latents [32g, +32) of the slice.
-          uint4* vp = reinterpret_cast<uint4*>(&sh.vbuf[w][16 * u + c][32 * g]);
-          vp[0] = __builtin_bit_cast(uint4, k01);
-          vp[1] = __builtin_bit_cast(uint4, k23);
-          vp[2] = __builtin_bit_cast(uint4, k45);
-          vp[3] = __builtin_bit_cast(uint4, k67);
+          const int vrow = 16 * u + c;
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g)) = __builtin_bit_cast(uint4, k01);
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g + 8)) = __builtin_bit_cast(uint4, k23);
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g + 16)) = __builtin_bit_cast(uint4, k45);
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g + 24)) = __builtin_bit_cast(uint4, k67);
         }
-        float4* rp = reinterpret_cast<float4*>(&sh.red[buf][kg][sl][lane][0]);
-        rp[0] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
-        rp[1] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
+        sh.red[buf][kg][sl][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
+        sh.red[buf][kg][sl][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
       }
       __syncthreads();
       if (!has_tile) continue;
@@ -380,9 +389,8 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         float4 rr[kSlices][2];
 #pragma unroll
         for (int ss = 0; ss < kSlices; ss++) {
-          const float4* rp = reinterpret_cast<const float4*>(&sh.red[buf][kg][ss][lane][0]);
-          rr[ss][0] = rp[0];
-          rr[ss][1] = rp[1];
+          rr[ss][0] = sh.red[buf][kg][ss][0][lane];
+          rr[ss][1] = sh.red[buf][kg][ss][1][lane];
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -431,9 +439,9 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 #pragma unroll
       for (int dt = 0; dt < 8; dt++) {
         const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            GLM53_LDS(i16x4, &sh.vbuf[w][tr_row][16 * dt + tr_col]));
+            GLM53_LDS(i16x4, vbuf_at(sh, w, tr_row, 16 * dt + tr_col)));
         const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            GLM53_LDS(i16x4, &sh.vbuf[w][16 + tr_row][16 * dt + tr_col]));
+            GLM53_LDS(i16x4, vbuf_at(sh, w, 16 + tr_row, 16 * dt + tr_col)));
         const i32x2 v0i = __builtin_bit_cast(i32x2, v0);
         const i32x2 v1i = __builtin_bit_cast(i32x2, v1);
         const uint4 vv = make_uint4(v0i[0], v0i[1], v1i[0], v1i[1]);
