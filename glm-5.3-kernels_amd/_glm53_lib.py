@@ -26,6 +26,11 @@ EXPORTED = (
     "glm53_sparse_mla_partials",
     "glm53_sparse_mla_merge",
     "glm53_moe_align_small",
+    "glm53_moe_w4a16_repack",
+    "glm53_moe_w4a16_gate_up",
+    "glm53_moe_w4a16_down",
+    "glm53_fused_moe_w4a16_workspace_bytes",
+    "glm53_fused_moe_w4a16",
 )
 
 _lib = None
@@ -72,6 +77,18 @@ def load():
     L.glm53_sparse_mla_merge.argtypes = [P, I64, I64, I64, I64, P, I64, I64, P]
     L.glm53_moe_align_small.restype = I
     L.glm53_moe_align_small.argtypes = [P, I, I64, P, P, P, P]
+    F = ctypes.c_float
+    L.glm53_moe_w4a16_repack.restype = I
+    L.glm53_moe_w4a16_repack.argtypes = [P, I64, I64, I64, P, P]
+    L.glm53_moe_w4a16_gate_up.restype = I
+    L.glm53_moe_w4a16_gate_up.argtypes = [P, I64, P, P, P, P, I64, I64, I64, I64, I64, F, P, P]
+    L.glm53_moe_w4a16_down.restype = I
+    L.glm53_moe_w4a16_down.argtypes = [P, P, P, P, I, I64, P, I64, I64, I64, I64, I64, I64, P, I64, P]
+    L.glm53_fused_moe_w4a16_workspace_bytes.restype = I64
+    L.glm53_fused_moe_w4a16_workspace_bytes.argtypes = [I64, I64, I64]
+    L.glm53_fused_moe_w4a16.restype = I
+    L.glm53_fused_moe_w4a16.argtypes = [P, I64, P, P, P, P, P, I, P, I64, I64, I64, I64, I64, F, P, I64,
+                                        P, I64, P]
     version = L.glm53_abi_version()
     if version != ABI_VERSION:
         raise ImportError(f"{LIB_PATH} has ABI version {version}, expected {ABI_VERSION}")

@@ -1,0 +1,436 @@
+// W4A16 group-32 MoE expert GEMMs for gfx950: the consumer of the small
+// route aligner at the GLM-5.3 decode shape (1..8 tokens, top-8 of 288
+// experts, hidden 4096, per-rank expert intermediate 512).
+//
+// The computation is the one vLLM's fused Marlin MoE performs at that call
+// site (profiles/sm74/titan_prefill/marlin.py:384-437 composes it from the
+// same pieces; its gate, marlin.py:247-295, fixes the geometry):
+//   c1[r]  = bf16(x[token(r)] . W13[e(r)]^T)               [R, 2N]
+//   c2[r]  = bf16(silu(min(gate, L)) * clamp(up, -L, L))   [R, N], gate = c1[r, :N], up = c1[r, N:]
+//   c3[r]  = bf16(w_r * (c2[r] . W2[e(r)]^T))               [R, K]
+//   out[t] = bf16(sum over the token's 8 routes of c3)      [T, K]
+// with W = (q - 8) * s: q an unsigned 4-bit code (uint4b8), s one bf16 scale
+// per 32 consecutive input features of an output row.
+//
+// Weight layout (glm53_moe_w4a16_repack): the checkpoint's int32
+// [E][n_out][K/8] words (word w of row n holds k = 8w + i in bits 4i) become
+// tiles [E][n_out/16][K/128][64 lanes][4 words].  Lane l of a tile holds
+// output row 16*tile + l%16; its word i holds k = 32*(4c + i) + 8*(l/16) +
+// [0, 8) for the tile's 128-feature chunk c, with k = 2j in bits 4j and k =
+// 2j + 1 in bits 16 + 4j.  So a 16-byte load per lane brings four groups of
+// the MFMA's B operand, and (word >> 4j) & 0x000F000F | 0x43004300 is the
+// bf16 pair (128 + q_2j, 128 + q_2j+1) with two VALU ops.  Scales stay in the
+// checkpoint's [E][n_out][K/32] bf16 layout.
+//
+// Per group of 32 features, D[m][n] = X[m][32] . B[32][n] runs on
+// v_mfma_f32_16x16x32_bf16 with A = the activation rows (m = route slot) and
+// B = the (128 + q) codes; a first MFMA with B = -136 everywhere seeds the
+// accumulator with -136 * sum(x), so D = sum x * (q - 8) exactly as the group
+// needs it, and the group's scale enters with one fp32 FMA per output:
+// lane (l/16, l%16) holds column n = l%16 and rows m = 4*(l/16) + [0, 4), so
+// each lane needs the single scale of its column.
+//
+// Gate/up kernel: one workgroup per (aligner block of 8 route slots, 16
+// intermediate columns); 8 wavefronts split K (128-feature chunks round
+// robin), each issues all of its weight, scale and activation loads before
+// the first MFMA, then the 8 partial tiles are summed in LDS in wave order.
+// Down kernel: one workgroup per (token, 16 output features); wavefront j
+// computes route slot j of the token (its expert's 16 rows over N), the 8
+// weighted results are summed in slot order.  Both kernels are deterministic.
+#include "glm53_common.h"
+
+namespace glm53 {
+namespace {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTileN = 16;        // output rows per tile
+constexpr int kChunkK = 128;      // features per 16-byte lane load (4 groups)
+constexpr int kGroup = 32;
+constexpr int kBatch = 4;         // chunks per wave whose loads are in flight together
+constexpr int kBlock = 8;         // route slots per aligner block
+constexpr uint32_t kMagic = 0x43004300u;   // bf16 pair (128, 128)
+constexpr uint32_t kMinus136 = 0xC308C308u;  // bf16 pair (-136, -136)
+
+// 0x000F000F in a VGPR.  With the mask in a register (and the magic in an
+// SGPR) the compiler forms one v_and_or_b32 per pair; with both as literals
+// it needs v_and + v_or (a VOP3 instruction takes no literal on gfx950).
+__device__ __forceinline__ uint32_t nibble_mask() {
+  uint32_t m;
+  asm volatile("v_mov_b32 %0, 0xf000f" : "=v"(m));
+  return m;
+}
+
+// The codes of one repacked word as the bf16x8 B operand (128 + q each).
+__device__ __forceinline__ bf16x8 codes_to_bf16(uint32_t v, uint32_t mask) {
+  uint4 r;
+  r.x = (v & mask) | kMagic;
+  r.y = ((v >> 4) & mask) | kMagic;
+  r.z = ((v >> 8) & mask) | kMagic;
+  r.w = ((v >> 12) & mask) | kMagic;
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ------------------------------------------------------------------ repack
+__global__ __launch_bounds__(256) void moe_w4a16_repack_kernel(const uint32_t* __restrict__ src,
+                                                               uint32_t* __restrict__ dst,
+                                                               int64_t total_words, int n_tiles,
+                                                               int k_chunks, int k_words) {
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (d >= total_words) return;
+  const int i = static_cast<int>(d & 3);
+  const int l = static_cast<int>((d >> 2) & 63);
+  const int64_t rest = d >> 8;                  // (e * n_tiles + tile) * k_chunks + c
+  const int c = static_cast<int>(rest % k_chunks);
+  const int64_t et = rest / k_chunks;           // e * n_tiles + tile
+  const int64_t row = et * kTileN + (l & 15);   // e * n_out + n
+  const uint32_t w = src[row * k_words + 4 * (4 * c + i) + (l >> 4)];
+  uint32_t o = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    o |= ((w >> (8 * j)) & 0xFu) << (4 * j);            // k = 2j
+    o |= ((w >> (8 * j + 4)) & 0xFu) << (16 + 4 * j);   // k = 2j + 1
+  }
+  dst[d] = o;
+  (void)n_tiles;
+}
+
+// ------------------------------------------------------------------ gate/up
+struct GateUpArgs {
+  const uint16_t* x;        // bf16 [T][K], row stride sx (elements)
+  int64_t sx;
+  const uint4* w13;         // repacked [E][2N/16][K/128][64] uint4
+  const uint16_t* s13;      // bf16 [E][2N][K/32]
+  const int32_t* sorted_ids;
+  const int32_t* expert_ids;
+  int num_routes;           // R = T * topk (padding value in sorted_ids)
+  int topk;
+  int num_experts;
+  int n_inter;              // N
+  int hidden;               // K
+  float clamp;              // +inf: no clamp
+  uint16_t* act;            // bf16 [R][N]
+};
+
+struct GateUpShared {
+  float red[kWaves][2][4][64];
+};
+
+__global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateUpArgs a) {
+  __shared__ GateUpShared sh;
+  const int b = blockIdx.x;
+  const int jt = blockIdx.y;
+  const int e = a.expert_ids[b];
+  if (e < 0 || e >= a.num_experts) return;   // unused aligner block (uniform)
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  const int q = lane >> 4, col = lane & 15;
+
+  // Route slot of this lane's A rows (m = col) and whether it holds a route.
+  const int sid = a.sorted_ids[kBlock * b + (col & 7)];
+  const bool row_ok = col < kBlock && sid < a.num_routes;
+  const uint16_t* xrow = a.x + static_cast<int64_t>(row_ok ? sid / a.topk : 0) * a.sx + 8 * q;
+
+  const int k_chunks = a.hidden / kChunkK;
+  const int k_groups = a.hidden / kGroup;
+  const int n_tiles13 = 2 * a.n_inter / kTileN;
+  const uint4* wg = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + jt) * k_chunks) * 64 + lane;
+  const uint4* wu = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + a.n_inter / kTileN + jt) * k_chunks) * 64 + lane;
+  const int ng = kTileN * jt + col;
+  const uint16_t* sg = a.s13 + (static_cast<int64_t>(e) * 2 * a.n_inter + ng) * k_groups;
+  const uint16_t* su = sg + static_cast<int64_t>(a.n_inter) * k_groups;
+
+  const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
+  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
+  const uint32_t mask = nibble_mask();
+
+  for (int c0 = w; c0 < k_chunks; c0 += kWaves * kBatch) {
+    uint4 kg[kBatch], ku[kBatch];
+    uint2 scg[kBatch], scu[kBatch];
+    uint4 xa[kBatch][4];
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      const int c = c0 + kWaves * u;
+      kg[u] = ku[u] = make_uint4(0, 0, 0, 0);
+      scg[u] = scu[u] = make_uint2(0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) xa[u][i] = make_uint4(0, 0, 0, 0);
+      if (c < k_chunks) {
+        kg[u] = wg[static_cast<int64_t>(c) * 64];
+        ku[u] = wu[static_cast<int64_t>(c) * 64];
+        scg[u] = *reinterpret_cast<const uint2*>(sg + 4 * c);
+        scu[u] = *reinterpret_cast<const uint2*>(su + 4 * c);
+        if (row_ok) {
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            xa[u][i] = *reinterpret_cast<const uint4*>(xrow + kChunkK * c + kGroup * i);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      if (c0 + kWaves * u >= k_chunks) break;   // uniform
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const bf16x8 xv = __builtin_bit_cast(bf16x8, xa[u][i]);
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
+        const f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(kg[u], i), mask), corr, 0, 0, 0);
+        const f32x4 du = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ku[u], i), mask), corr, 0, 0, 0);
+        const uint32_t pg = i < 2 ? scg[u].x : scg[u].y;
+        const uint32_t pu = i < 2 ? scu[u].x : scu[u].y;
+        const float s_g = __uint_as_float((i & 1) ? (pg & 0xFFFF0000u) : (pg << 16));
+        const float s_u = __uint_as_float((i & 1) ? (pu & 0xFFFF0000u) : (pu << 16));
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          acc_g[r] = __builtin_fmaf(s_g, dg[r], acc_g[r]);
+          acc_u[r] = __builtin_fmaf(s_u, du[r], acc_u[r]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    sh.red[w][0][r][lane] = acc_g[r];
+    sh.red[w][1][r][lane] = acc_u[r];
+  }
+  __syncthreads();
+  if (threadIdx.x < kTileN * kBlock) {
+    const int n = threadIdx.x & 15;
+    const int m = threadIdx.x >> 4;   // route slot 0..7: lane n + 16*(m/4), element m%4
+    const int slot = a.sorted_ids[kBlock * b + m];
+    if (slot < a.num_routes) {
+      float g = 0.f, up = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ww++) {
+        g += sh.red[ww][0][m & 3][n + 16 * (m >> 2)];
+        up += sh.red[ww][1][m & 3][n + 16 * (m >> 2)];
+      }
+      g = fminf(bf16_round(g), a.clamp);
+      up = fminf(fmaxf(bf16_round(up), -a.clamp), a.clamp);
+      const float v = g / (1.0f + expf(-g)) * up;
+      a.act[static_cast<int64_t>(slot) * a.n_inter + kTileN * jt + n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ down
+struct DownArgs {
+  const uint16_t* act;      // bf16 [T * topk][N]
+  const uint4* w2;          // repacked [E][K/16][N/128][64] uint4
+  const uint16_t* s2;       // bf16 [E][K][N/32]
+  const void* topk_ids;     // [T][topk] int32 / int64, row stride sid_t
+  int ids_i64;
+  int64_t sid_t;
+  const float* topk_w;      // fp32 [T][topk], row stride sw_t
+  int64_t sw_t;
+  int topk;
+  int num_experts;
+  int n_inter;              // N (the reduction length here)
+  int hidden;               // K (output features)
+  uint16_t* out;            // bf16 [T][K], row stride so
+  int64_t so;
+};
+
+__global__ __launch_bounds__(kThreads) void moe_w4a16_down_kernel(const DownArgs a) {
+  __shared__ float part[kWaves][kTileN];
+  const int nt = blockIdx.x;
+  const int t = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  const int q = lane >> 4, col = lane & 15;
+  const int k_chunks = a.n_inter / kChunkK;
+  const int k_groups = a.n_inter / kGroup;
+  const int n_tiles2 = a.hidden / kTileN;
+  const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
+  const uint32_t mask = nibble_mask();
+
+  for (int j = w; j < a.topk; j += kWaves) {
+    int64_t raw = a.ids_i64 ? static_cast<const int64_t*>(a.topk_ids)[t * a.sid_t + j]
+                            : static_cast<int64_t>(static_cast<const int32_t*>(a.topk_ids)[t * a.sid_t + j]);
+    const bool ok = uniform(raw >= 0 && raw < a.num_experts);   // the same id in every lane
+    float y = 0.f;
+    if (ok) {
+      const int e = uniform(static_cast<int>(raw));
+      const uint4* wp = a.w2 + ((static_cast<int64_t>(e) * n_tiles2 + nt) * k_chunks) * 64 + lane;
+      const uint16_t* sp = a.s2 + (static_cast<int64_t>(e) * a.hidden + kTileN * nt + col) * k_groups;
+      const uint16_t* ar = a.act + (static_cast<int64_t>(t) * a.topk + j) * a.n_inter + 8 * q;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int c0 = 0; c0 < k_chunks; c0 += kBatch) {
+        uint4 kw[kBatch];
+        uint2 sc[kBatch];
+        uint4 xa[kBatch][4];
+#pragma unroll
+        for (int u = 0; u < kBatch; u++) {
+          const int c = c0 + u;
+          kw[u] = make_uint4(0, 0, 0, 0);
+          sc[u] = make_uint2(0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; i++) xa[u][i] = make_uint4(0, 0, 0, 0);
+          if (c < k_chunks) {
+            kw[u] = wp[static_cast<int64_t>(c) * 64];
+            sc[u] = *reinterpret_cast<const uint2*>(sp + 4 * c);
+            if (col == 0) {
+#pragma unroll
+              for (int i = 0; i < 4; i++)
+                xa[u][i] = *reinterpret_cast<const uint4*>(ar + kChunkK * c + kGroup * i);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; u++) {
+          if (c0 + u >= k_chunks) break;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const bf16x8 xv = __builtin_bit_cast(bf16x8, xa[u][i]);
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
+            const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(kw[u], i), mask), corr, 0, 0, 0);
+            const uint32_t p = i < 2 ? sc[u].x : sc[u].y;
+            const float s = __uint_as_float((i & 1) ? (p & 0xFFFF0000u) : (p << 16));
+            acc[0] = __builtin_fmaf(s, d[0], acc[0]);   // row m = 0: lanes 0..15, element 0
+          }
+        }
+      }
+      const float tw = a.topk_w[t * a.sw_t + j];
+      y = bf16_round(tw * acc[0]);
+    }
+    if (lane < kTileN) part[w][lane] = y;
+  }
+  __syncthreads();
+  if (threadIdx.x < kTileN) {
+    float s = 0.f;
+    const int nw = a.topk < kWaves ? a.topk : kWaves;
+    for (int ww = 0; ww < nw; ww++) s += part[ww][threadIdx.x];
+    a.out[t * a.so + kTileN * nt + threadIdx.x] = static_cast<uint16_t>(f32_to_bf16_bits(s));
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+}  // namespace glm53
+
+using namespace glm53;
+
+extern "C" int glm53_moe_align_small(const void* topk_ids, int ids_is_i64, int64_t num_routes,
+                                     int32_t* sorted_ids, int32_t* expert_ids,
+                                     int32_t* num_tokens_post_padded, void* stream);
+
+extern "C" int glm53_moe_w4a16_repack(const void* w_packed, int64_t num_experts, int64_t n_out,
+                                      int64_t k, void* out, void* stream) {
+  if (!w_packed || !out) return GLM53_ERR_NULL_POINTER;
+  if (num_experts < 1 || n_out < kTileN || n_out % kTileN || k < kChunkK || k % kChunkK)
+    return GLM53_ERR_BAD_SHAPE;
+  if (!aligned16(out) || (reinterpret_cast<uintptr_t>(w_packed) & 3)) return GLM53_ERR_MISALIGNED;
+  const int64_t total = num_experts * n_out * (k / 8);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(moe_w4a16_repack_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint32_t*>(w_packed),
+                     static_cast<uint32_t*>(out), total, static_cast<int>(n_out / kTileN),
+                     static_cast<int>(k / kChunkK), static_cast<int>(k / 8));
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int glm53_moe_w4a16_gate_up(const void* x, int64_t sx, const void* w13, const void* s13,
+                                       const int32_t* sorted_ids, const int32_t* expert_ids,
+                                       int64_t num_routes, int64_t topk, int64_t num_experts,
+                                       int64_t n_inter, int64_t hidden, float clamp_limit, void* act,
+                                       void* stream) {
+  if (!x || !w13 || !s13 || !sorted_ids || !expert_ids || !act) return GLM53_ERR_NULL_POINTER;
+  if (num_routes < 1 || num_routes > (1 << 24) || topk < 1 || num_experts < 1 || n_inter < kTileN ||
+      n_inter % kTileN || hidden < kChunkK || hidden % kChunkK || sx < hidden || !(clamp_limit > 0.f))
+    return GLM53_ERR_BAD_SHAPE;
+  if (!aligned16(x) || sx % 8 || !aligned16(w13) || (reinterpret_cast<uintptr_t>(s13) & 7) || (reinterpret_cast<uintptr_t>(act) & 1))
+    return GLM53_ERR_MISALIGNED;
+  GateUpArgs a{static_cast<const uint16_t*>(x), sx, static_cast<const uint4*>(w13),
+               static_cast<const uint16_t*>(s13), sorted_ids, expert_ids, static_cast<int>(num_routes),
+               static_cast<int>(topk), static_cast<int>(num_experts), static_cast<int>(n_inter),
+               static_cast<int>(hidden), clamp_limit, static_cast<uint16_t*>(act)};
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(moe_w4a16_gate_up_kernel, dim3(static_cast<unsigned>(num_routes), static_cast<unsigned>(n_inter / kTileN)),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int glm53_moe_w4a16_down(const void* act, const void* w2, const void* s2, const void* topk_ids,
+                                    int ids_is_i64, int64_t sid_t, const float* topk_weights, int64_t sw_t,
+                                    int64_t num_tokens, int64_t topk, int64_t num_experts, int64_t n_inter,
+                                    int64_t hidden, void* out, int64_t so, void* stream) {
+  if (!act || !w2 || !s2 || !topk_ids || !topk_weights || !out) return GLM53_ERR_NULL_POINTER;
+  if (num_tokens < 1 || num_tokens > 65535 || topk < 1 || topk > kWaves || num_experts < 1 ||
+      n_inter < kChunkK || n_inter % kChunkK || hidden < kTileN || hidden % kTileN || sid_t < topk ||
+      sw_t < topk || so < hidden)
+    return GLM53_ERR_BAD_SHAPE;
+  if (!aligned16(act) || !aligned16(w2) || (reinterpret_cast<uintptr_t>(s2) & 7) || (reinterpret_cast<uintptr_t>(out) & 1))
+    return GLM53_ERR_MISALIGNED;
+  DownArgs a{static_cast<const uint16_t*>(act), static_cast<const uint4*>(w2), static_cast<const uint16_t*>(s2),
+             topk_ids, ids_is_i64, sid_t, topk_weights, sw_t, static_cast<int>(topk),
+             static_cast<int>(num_experts), static_cast<int>(n_inter), static_cast<int>(hidden),
+             static_cast<uint16_t*>(out), so};
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(moe_w4a16_down_kernel, dim3(static_cast<unsigned>(hidden / kTileN), static_cast<unsigned>(num_tokens)),
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Workspace of glm53_fused_moe_w4a16: aligner outputs, then the activations.
+namespace {
+constexpr int64_t kAlignBytes = 256;
+int64_t round_up(int64_t v) { return (v + kAlignBytes - 1) / kAlignBytes * kAlignBytes; }
+struct FusedLayout {
+  int64_t sorted, experts, postpad, act, total;
+};
+FusedLayout fused_layout(int64_t routes, int64_t n_inter) {
+  FusedLayout l;
+  l.sorted = 0;
+  l.experts = round_up(routes * kBlock * 4);
+  l.postpad = l.experts + round_up(routes * 4);
+  l.act = l.postpad + kAlignBytes;
+  l.total = l.act + round_up(routes * n_inter * 2);
+  return l;
+}
+constexpr int64_t kAlignerExperts = 288;
+constexpr int64_t kAlignerTopk = 8;
+constexpr int64_t kAlignerMaxTokens = 8;
+}  // namespace
+
+extern "C" int64_t glm53_fused_moe_w4a16_workspace_bytes(int64_t num_tokens, int64_t topk, int64_t n_inter) {
+  if (num_tokens < 1 || topk < 1 || n_inter < 1) return 0;
+  return fused_layout(num_tokens * topk, n_inter).total;
+}
+
+extern "C" int glm53_fused_moe_w4a16(const void* x, int64_t sx, const void* w13, const void* s13,
+                                     const void* w2, const void* s2, const void* topk_ids, int ids_is_i64,
+                                     const float* topk_weights, int64_t num_tokens, int64_t topk,
+                                     int64_t num_experts, int64_t n_inter, int64_t hidden, float clamp_limit,
+                                     void* workspace, int64_t workspace_bytes, void* out, int64_t so,
+                                     void* stream) {
+  if (!x || !w13 || !s13 || !w2 || !s2 || !topk_ids || !topk_weights || !out || !workspace)
+    return GLM53_ERR_NULL_POINTER;
+  if (num_tokens < 1 || num_tokens > kAlignerMaxTokens || topk != kAlignerTopk || num_experts != kAlignerExperts)
+    return GLM53_ERR_BAD_SHAPE;
+  const int64_t routes = num_tokens * topk;
+  const FusedLayout l = fused_layout(routes, n_inter);
+  if (workspace_bytes < l.total) return GLM53_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return GLM53_ERR_MISALIGNED;
+  char* ws = static_cast<char*>(workspace);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + l.sorted);
+  int32_t* experts = reinterpret_cast<int32_t*>(ws + l.experts);
+  int32_t* postpad = reinterpret_cast<int32_t*>(ws + l.postpad);
+  void* act = ws + l.act;
+  int rc = glm53_moe_align_small(topk_ids, ids_is_i64, routes, sorted, experts, postpad, stream);
+  if (rc) return rc;
+  rc = glm53_moe_w4a16_gate_up(x, sx, w13, s13, sorted, experts, routes, topk, num_experts, n_inter, hidden,
+                               clamp_limit, act, stream);
+  if (rc) return rc;
+  return glm53_moe_w4a16_down(act, w2, s2, topk_ids, ids_is_i64, topk, topk_weights, topk, num_tokens, topk,
+                              num_experts, n_inter, hidden, out, so, stream);
+}

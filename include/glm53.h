@@ -217,6 +217,77 @@ int glm53_moe_align_small(const void* topk_ids, int ids_is_i64,
                           int32_t* expert_ids,
                           int32_t* num_tokens_post_padded, void* stream);
 
+/*
+ * W4A16 group-32 MoE expert GEMMs: the consumer of glm53_moe_align_small.
+ * Replace the two moe_wna16_marlin_gemm launches, the activation and the
+ * moe_sum of vLLM's fused Marlin MoE at the GLM-5.3 call site (the call
+ * sequence profiles/sm74/titan_prefill/marlin.py:384-437, gated on
+ * marlin.py:247-295: bf16 activations, uint4b8 weights with bf16 group-32
+ * scales and no zero points, SiLU with clamp, router weight on the output;
+ * the aligner's call site integration/patch_moe_align.py:17-44).
+ *
+ * With W = (q - 8) * s (q the unsigned 4-bit code, s the bf16 scale of its
+ * 32-feature group) and route r = t * topk + j of token t with expert
+ * e = topk_ids[t, j] and weight w = topk_weights[t, j]:
+ *   c1[r] = bf16(x[t] . W13[e]^T)                         (2N values)
+ *   c2[r] = bf16(silu(min(g, L)) * min(max(u, -L), L))    g = c1[r, :N], u = c1[r, N:]
+ *   c3[r] = bf16(w * (c2[r] . W2[e]^T))                   (K values)
+ *   out[t] = bf16(c3[t*topk] + ... + c3[t*topk + topk-1]) (fp32 sum in slot order)
+ * Routes whose expert lies outside [0, num_experts) contribute 0.
+ * L = clamp_limit (> 0; +inf for plain SiLU-and-multiply).
+ *
+ * Weights: checkpoint int32 [E][n_out][K/8] (word w of row n holds k = 8w+i
+ * in bits 4i, the GPTQ / compressed-tensors packing) are repacked once by
+ * glm53_moe_w4a16_repack into the kernels' tile order (same size, int32
+ * [E][n_out/16][K/128][64][4]); W13 is [E][2N][K] (gate rows, then up rows),
+ * W2 is [E][K][N].  Scales are used as the checkpoint holds them: bf16
+ * [E][n_out][K/32].  N and K are multiples of 128 (K) and 16 (N) for W13, N
+ * a multiple of 128 for W2.
+ */
+/* Repack [E][n_out][k/8] int32 words (w_packed, 4-byte aligned) into the
+ * tile order at out (16-byte aligned, same byte size).  n_out % 16 == 0,
+ * k % 128 == 0. */
+int glm53_moe_w4a16_repack(const void* w_packed, int64_t num_experts,
+                           int64_t n_out, int64_t k, void* out, void* stream);
+
+/* c2 for every route of the aligner's blocks: one workgroup per (8-slot
+ * block b with expert_ids[b] in [0, E), 16 intermediate columns); slots
+ * holding num_routes are padding.  x bf16 [T][hidden], row stride sx
+ * elements (16-byte aligned rows); act bf16 [num_routes][n_inter]. */
+int glm53_moe_w4a16_gate_up(const void* x, int64_t sx, const void* w13,
+                            const void* s13, const int32_t* sorted_ids,
+                            const int32_t* expert_ids, int64_t num_routes,
+                            int64_t topk, int64_t num_experts,
+                            int64_t n_inter, int64_t hidden,
+                            float clamp_limit, void* act, void* stream);
+
+/* out for every token: one workgroup per (16 output features, token), the
+ * token's topk (<= 8) routes summed in slot order.  topk_ids int32 or int64
+ * (ids_is_i64) [T][topk] with row stride sid_t; topk_weights fp32 [T][topk]
+ * with row stride sw_t; out bf16 [T][hidden], row stride so. */
+int glm53_moe_w4a16_down(const void* act, const void* w2, const void* s2,
+                         const void* topk_ids, int ids_is_i64, int64_t sid_t,
+                         const float* topk_weights, int64_t sw_t,
+                         int64_t num_tokens, int64_t topk,
+                         int64_t num_experts, int64_t n_inter,
+                         int64_t hidden, void* out, int64_t so, void* stream);
+
+/* Bytes of the workspace glm53_fused_moe_w4a16 needs (aligner outputs and
+ * the c2 activations). */
+int64_t glm53_fused_moe_w4a16_workspace_bytes(int64_t num_tokens,
+                                              int64_t topk, int64_t n_inter);
+
+/* Aligner + gate/up + down for 1..8 tokens, top-8, 288 experts (the
+ * aligner's contract); topk_ids and topk_weights contiguous [T][8]. */
+int glm53_fused_moe_w4a16(const void* x, int64_t sx, const void* w13,
+                          const void* s13, const void* w2, const void* s2,
+                          const void* topk_ids, int ids_is_i64,
+                          const float* topk_weights, int64_t num_tokens,
+                          int64_t topk, int64_t num_experts, int64_t n_inter,
+                          int64_t hidden, float clamp_limit, void* workspace,
+                          int64_t workspace_bytes, void* out, int64_t so,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

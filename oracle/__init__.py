@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 CPU-baseline leg of bench.py, always as the checker.  The product modules
-(titan_kv, titan_mla, titan_moe_align) never import it.
+(titan_kv, titan_mla, titan_moe_align, titan_moe_w4a16, sparse_utils) never
+import it.
 
 The arithmetic lives in glm53_oracle.c (built by oracle/Makefile into
 liboracle.so); this module wraps it for numpy arrays and restates the two
@@ -33,6 +34,15 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
   restatement), invariants (split-count invariance, all-masked -> 0, masking
   of positive out-of-range indices, permutation invariance, one valid row,
   q = 0 gives the mean row).
+* moe_w4a16 (+ unpack_w4 / pack_w4 / repack_w4a16), the expert GEMMs after
+  the aligner (vLLM's fused Marlin MoE at integration/patch_moe_align.py:
+  17-44, composed as profiles/sm74/titan_prefill/marlin.py:384-437): bit
+  brute force of the packing and of the tile order, closed forms from
+  uniform weights and from single codes per expert (every index of the
+  layer), the SiLU clamp, route invariants and an independent torch
+  formulation (tests/test_oracle_moe_w4a16.py).  The clamp's exact form
+  (gate clamped above, up clamped both ways, limit 10) is vLLM's and is not
+  in the reference: parity of that detail with vLLM is unpinned.
 """
 from __future__ import annotations
 
@@ -277,3 +287,94 @@ def expand_pools(pool_ids: np.ndarray, seq_lens, pool_size: int, out_cols: int |
             out[:, lo:hi] = tail[:, : hi - lo]
     return out.astype(np.int32)
 
+
+
+# --------------------------------------------------------------------------
+# W4A16 group-32 MoE expert GEMMs (the consumer of moe_align; vLLM's fused
+# Marlin MoE at integration/patch_moe_align.py:17-44, composed as in
+# profiles/sm74/titan_prefill/marlin.py:384-437)
+# --------------------------------------------------------------------------
+
+def unpack_w4(words: np.ndarray) -> np.ndarray:
+    """int32 [..., K/8] GPTQ-packed words -> uint8 codes [..., K]: code k of
+    a row is bits 4*(k % 8) .. +3 of word k // 8."""
+    w = np.ascontiguousarray(words).view(np.uint32)
+    shifts = 4 * np.arange(8, dtype=np.uint32)
+    return ((w[..., None] >> shifts) & 0xF).astype(np.uint8).reshape(*w.shape[:-1], 8 * w.shape[-1])
+
+
+def pack_w4(codes: np.ndarray) -> np.ndarray:
+    """Inverse of unpack_w4: uint8 codes [..., K] (values 0..15) -> int32 [..., K/8]."""
+    c = np.asarray(codes, dtype=np.uint32).reshape(*codes.shape[:-1], codes.shape[-1] // 8, 8)
+    return (c << (4 * np.arange(8, dtype=np.uint32))).sum(axis=-1, dtype=np.uint32).view(np.int32)
+
+
+def repack_w4a16(words: np.ndarray) -> np.ndarray:
+    """The kernels' tile order (glm53_moe_w4a16_repack): [E, n_out, K/8] ->
+    int32 [E, n_out/16, K/128, 64, 4].  Lane l of tile (e, nt, c) holds row
+    16*nt + l%16; its word i holds codes k = 32*(4c+i) + 8*(l//16) + 2j in
+    bits 4j and k + 1 in bits 16 + 4j (j = 0..3)."""
+    codes = unpack_w4(words)                         # [E, n, K]
+    E, n, K = codes.shape
+    c = codes.reshape(E, n // 16, 16, K // 128, 4, 4, 8)   # e, nt, row, chunk, i, q, kk
+    c = c.transpose(0, 1, 3, 5, 2, 4, 6).astype(np.uint32)  # e, nt, chunk, q, row, i, kk
+    shift = np.array([0, 16, 4, 20, 8, 24, 12, 28], dtype=np.uint32)
+    w = (c << shift).sum(axis=-1, dtype=np.uint32)          # e, nt, chunk, q, row, i
+    return w.reshape(E, n // 16, K // 128, 64, 4).view(np.int32)
+
+
+def _dequant(words: np.ndarray, scales_u16: np.ndarray) -> np.ndarray:
+    """(q - 8) * s in float64 (exact), [n_out, K]."""
+    q = unpack_w4(words).astype(np.float64) - 8.0
+    s = bf16_to_f32(scales_u16).astype(np.float64)
+    return q * np.repeat(s, 32, axis=-1)
+
+
+def moe_w4a16(x_u16: np.ndarray, w13: np.ndarray, s13: np.ndarray, w2: np.ndarray, s2: np.ndarray,
+              topk_weights: np.ndarray, topk_ids: np.ndarray, clamp_limit: float | None = 10.0,
+              cache: dict | None = None):
+    """The MoE layer for tokens x (bf16 bits [T, K]) and routes (topk_ids,
+    topk_weights [T, topk]); weights in checkpoint packing (w13 int32 [E, 2N,
+    K/8], s13 bf16 bits [E, 2N, K/32], w2 [E, K, N/8], s2 [E, K, N/32]).
+
+    Rounding points (those of the fused Marlin MoE: bf16 intermediate
+    buffers, moe_sum over fp32): c1 = bf16(x . W13^T) with an exact float64
+    dot, c2 = bf16(silu(min(g, L)) * clip(u, -L, L)) computed in fp32,
+    c3 = bf16(fp32(w) * fp32(c2 . W2^T)), out = bf16 of the fp32 sum of the
+    token's c3 in slot order.  A route whose expert is outside [0, E) gives
+    c3 = 0.  Returns (out bf16 bits [T, K], c2 bf16 bits [T*topk, N] with
+    zero rows for dropped routes).  `cache` (a dict, optional) keeps the
+    dequantised experts between calls on the same weights."""
+    L = np.float32(np.inf if clamp_limit is None else clamp_limit)
+    x = bf16_to_f32(x_u16).astype(np.float64)
+    E = w13.shape[0]
+    N = w13.shape[1] // 2
+    T, topk = topk_ids.shape
+    K = x.shape[1]
+    ids = np.asarray(topk_ids, dtype=np.int64)
+    tw = np.asarray(topk_weights, dtype=np.float32)
+    act = np.zeros((T * topk, N), dtype=np.uint16)
+    c3 = np.zeros((T, topk, K), dtype=np.float32)
+    cache = {} if cache is None else cache
+    for t in range(T):
+        for j in range(topk):
+            e = int(ids[t, j])
+            if not 0 <= e < E:
+                continue
+            if e not in cache:   # (q - 8) * s is exact in fp32 (4-bit code times bf16 scale)
+                cache[e] = (_dequant(w13[e], s13[e]).astype(np.float32),
+                            _dequant(w2[e], s2[e]).astype(np.float32))
+            W13, W2 = (m.astype(np.float64) for m in cache[e])
+            c1 = bf16_to_f32(f32_to_bf16((W13 @ x[t]).astype(np.float32)))
+            g = np.minimum(c1[:N], L)
+            u = np.clip(c1[N:], -L, L)
+            with np.errstate(over="ignore"):
+                c2 = g / (np.float32(1) + np.exp(-g)) * u
+            c2b = f32_to_bf16(c2.astype(np.float32))
+            act[t * topk + j] = c2b
+            y = (W2 @ bf16_to_f32(c2b).astype(np.float64)).astype(np.float32)
+            c3[t, j] = bf16_to_f32(f32_to_bf16(tw[t, j] * y))
+    out = np.zeros((T, K), dtype=np.float32)
+    for j in range(topk):
+        out += c3[:, j]
+    return f32_to_bf16(out), act

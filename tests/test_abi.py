@@ -120,7 +120,8 @@ def test_import_does_not_touch_cuda():
         for fname, exported in (("titan_kv.py", "store_int8"),
                                 ("titan_mla.py", "triton_mla_sparse_attention"),
                                 ("titan_moe_align.py", "titan_moe_align_small"),
-                                ("sparse_utils.py", "triton_convert_req_index_to_global_index")):
+                                ("sparse_utils.py", "triton_convert_req_index_to_global_index"),
+                                ("titan_moe_w4a16.py", "fused_moe_w4a16")):
             spec = importlib.util.spec_from_file_location("isolated_" + fname[:-3], pkg / fname)
             mod = importlib.util.module_from_spec(spec)
             spec.loader.exec_module(mod)
@@ -186,3 +187,82 @@ def test_convert_contract_on_cpu():
         conv(req.long(), bt, idx, BLOCK_SIZE=64, NUM_TOPK_TOKENS=256)
     with pytest.raises(NotImplementedError):
         conv(req, bt, idx, BLOCK_SIZE=64, NUM_TOPK_TOKENS=256, HAS_PREFILL_WORKSPACE=True)
+
+
+def test_moe_w4a16_host_errors():
+    """Argument errors of the W4A16 MoE entry points are caught on the host
+    before any launch (no device needed)."""
+    import _glm53_lib
+    L = _glm53_lib.load()
+    fake = ctypes.c_void_p(0x10000)
+    mis = ctypes.c_void_p(0x10008)
+    # repack: null, shapes, alignment
+    assert L.glm53_moe_w4a16_repack(None, 288, 1024, 4096, fake, None) == -1
+    assert L.glm53_moe_w4a16_repack(fake, 288, 1000, 4096, fake, None) == -2
+    assert L.glm53_moe_w4a16_repack(fake, 288, 1024, 4000, fake, None) == -2
+    assert L.glm53_moe_w4a16_repack(fake, 0, 1024, 4096, fake, None) == -2
+    assert L.glm53_moe_w4a16_repack(fake, 288, 1024, 4096, mis, None) == -3
+    # gate/up: x, sx, w13, s13, sorted, experts, R, topk, E, N, K, clamp, act, stream
+    args = [fake, 4096, fake, fake, fake, fake, 64, 8, 288, 512, 4096, 10.0, fake, None]
+    bad = lambda i, v: L.glm53_moe_w4a16_gate_up(*(args[:i] + [v] + args[i + 1:]))
+    assert bad(0, None) == -1
+    assert bad(9, 500) == -2            # N not a multiple of 16
+    assert bad(10, 4000) == -2          # K not a multiple of 128
+    assert bad(1, 4000) == -2           # row stride below K
+    assert bad(11, 0.0) == -2           # clamp limit must be > 0
+    assert bad(11, float("nan")) == -2
+    assert bad(0, mis) == -3
+    assert bad(1, 4100) == -3           # row stride breaks 16-byte rows
+    # down: act, w2, s2, ids, i64, sid_t, w, sw_t, T, topk, E, N, K, out, so, stream
+    args = [fake, fake, fake, fake, 0, 8, fake, 8, 8, 8, 288, 512, 4096, fake, 4096, None]
+    bad = lambda i, v: L.glm53_moe_w4a16_down(*(args[:i] + [v] + args[i + 1:]))
+    assert bad(6, None) == -1
+    assert bad(9, 9) == -2              # more than 8 routes per token
+    assert bad(11, 500) == -2           # N not a multiple of 128
+    assert bad(5, 4) == -2              # ids row stride below topk
+    assert bad(0, mis) == -3
+    # fused: the aligner's contract (1..8 tokens, top-8, 288 experts) and the workspace
+    ws = L.glm53_fused_moe_w4a16_workspace_bytes(8, 8, 512)
+    assert ws >= 64 * 512 * 2 + 64 * 8 * 4
+    args = [fake, 4096, fake, fake, fake, fake, fake, 0, fake, 8, 8, 288, 512, 4096, 10.0, fake, ws, fake,
+            4096, None]
+    bad = lambda i, v: L.glm53_fused_moe_w4a16(*(args[:i] + [v] + args[i + 1:]))
+    assert bad(9, 9) == -2              # 9 tokens
+    assert bad(10, 4) == -2             # top-4
+    assert bad(11, 256) == -2           # 256 experts
+    assert bad(16, ws - 1) == -4
+    assert bad(15, None) == -1
+
+
+def test_moe_w4a16_contract_errors_on_cpu():
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16, repack_w4a16
+    x = torch.zeros(2, 4096, dtype=torch.bfloat16)
+    w13 = torch.zeros(288, 64, 32, 64, 4, dtype=torch.int32)
+    w2 = torch.zeros(288, 256, 4, 64, 4, dtype=torch.int32)
+    s13 = torch.zeros(288, 1024, 128, dtype=torch.bfloat16)
+    s2 = torch.zeros(288, 4096, 16, dtype=torch.bfloat16)
+    tw = torch.zeros(2, 8)
+    ids = torch.zeros(2, 8, dtype=torch.int32)
+    call = lambda **kw: fused_moe_w4a16(**{**dict(hidden_states=x, w13=w13, w2=w2, w13_scale=s13,
+                                                  w2_scale=s2, topk_weights=tw, topk_ids=ids), **kw})
+    with pytest.raises(ValueError, match="expert_map"):
+        call(expert_map=torch.arange(288))
+    with pytest.raises(ValueError, match="router weight"):
+        call(apply_router_weight_on_input=True)
+    with pytest.raises(ValueError, match="tokens"):
+        call(hidden_states=torch.zeros(9, 4096, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="topk_ids"):
+        call(topk_ids=torch.zeros(2, 4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="topk_weights"):
+        call(topk_weights=torch.zeros(2, 8, dtype=torch.float16))
+    with pytest.raises(ValueError, match="experts"):
+        call(w13=w13[:256], w2=w2[:256])
+    with pytest.raises(ValueError, match="w13_scale"):
+        call(w13_scale=s13[:, :, :64])
+    with pytest.raises(ValueError, match="w2"):
+        call(w2=torch.zeros(288, 256, 4, 64, 2, dtype=torch.int32))
+    with pytest.raises(ValueError, match="clamp_limit"):
+        call(clamp_limit=0.0)
+    with pytest.raises(ValueError):
+        repack_w4a16(torch.zeros(288, 1000, 512, dtype=torch.int32))

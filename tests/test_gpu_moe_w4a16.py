@@ -1,0 +1,195 @@
+"""GPU parity of the W4A16 group-32 MoE layer (repack, gate/up + SiLU with
+clamp, down + router weights + route sum) against the oracle, at the GLM-5.3
+TP4 decode shape: 288 experts, hidden 4096, intermediate 512, top-8, 1..8
+tokens, the reference aligner's seven routing patterns
+(benchmarks/moe_align.py:49-55).
+
+Tolerances.  The kernels sum each 32-feature group on the matrix cores and
+the groups in fp32 in another order than the oracle's exact dot, so a bf16
+rounding point (c1, c2, c3) may land one ulp apart.  c2 (the activation) is
+checked elementwise to |d| <= 2^-6 |ref| + 2^-10 (two bf16 ulps plus a
+floor for values near zero); the layer output elementwise to
+|d| <= 2^-7 |ref| + 2e-2 (one bf16 ulp of the value over the attention's
+max-abs bar, which alone fits outputs of unit scale) and to mean-abs <=
+2e-3 * max(1, mean |ref|).  The repack is integer work and is bit-exact."""
+import random
+
+import numpy as np
+import pytest
+
+import workloads as W
+from conftest import log_case
+
+pytestmark = pytest.mark.gpu
+
+PATTERNS = ("distinct", "shared_top8", "random_top8", "all_one_expert", "seven_experts", "invalid_mixed",
+            "all_invalid")
+
+
+@pytest.fixture(scope="module")
+def moe(cuda, oracle):
+    import torch
+    from titan_moe_w4a16 import repack_w4a16
+    log_case("moe layer: build 288 x (1024 x 4096 + 4096 x 512) W4A16 weights")
+    lay = W.moe_w4a16_layer(cuda, seed=W.SEED_FIXTURE)
+    dev = {"w13": repack_w4a16(lay["w13_packed"]), "w2": repack_w4a16(lay["w2_packed"]),
+           "w13_scale": lay["w13_scale"], "w2_scale": lay["w2_scale"]}
+    host = {k: v.cpu().numpy() if v.dtype != torch.bfloat16 else v.view(torch.int16).cpu().numpy().view(np.uint16)
+            for k, v in lay.items()}
+    torch.cuda.synchronize()
+    return {"dev": dev, "host": host, "packed": lay, "cache": {}}
+
+
+def run_oracle(oracle, moe, x, ids, tw, clamp=10.0):
+    import torch
+    h = moe["host"]
+    xs = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    return oracle.moe_w4a16(xs, h["w13_packed"], h["w13_scale"], h["w2_packed"], h["w2_scale"],
+                            tw.cpu().numpy(), ids.cpu().numpy(), clamp_limit=clamp, cache=moe["cache"])
+
+
+def assert_out_close(got, want_u16, oracle, what):
+    g = got.float().cpu().numpy()
+    w = oracle.bf16_to_f32(want_u16)
+    err = np.abs(g - w)
+    excess = err - (2.0 ** -7 * np.abs(w) + 2e-2)
+    mean_bar = 2e-3 * max(1.0, float(np.abs(w).mean()))
+    assert excess.max() <= 0 and err.mean() <= mean_bar, \
+        f"{what}: max {err.max():.3e} (excess {excess.max():.3e}) mean {err.mean():.3e} (bar {mean_bar:.2e})"
+    return err
+
+
+def assert_act_close(got, want_u16, rows, oracle, what):
+    g = got.float().cpu().numpy()[rows]
+    w = oracle.bf16_to_f32(want_u16)[rows]
+    bad = np.abs(g - w) > 2.0 ** -6 * np.abs(w) + 2.0 ** -10
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} c2 values off, e.g. {g[bad][:4]} vs {w[bad][:4]}"
+
+
+def test_repack_bit_exact(cuda, oracle, moe):
+    import torch
+    from titan_moe_w4a16 import repack_w4a16
+    g = torch.Generator(device=cuda).manual_seed(5)
+    small = torch.randint(0, 256, (3, 48, 192), generator=g, device=cuda, dtype=torch.uint8).view(torch.int32)
+    log_case("repack [3, 48, 48] words")
+    got = repack_w4a16(small).cpu().numpy()
+    assert np.array_equal(got, oracle.repack_w4a16(small.cpu().numpy()))
+    for name in ("w13", "w2"):
+        want = oracle.repack_w4a16(moe["host"][name + "_packed"][[0, 141, 287]])
+        assert np.array_equal(moe["dev"][name][[0, 141, 287]].cpu().numpy(), want), name
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+@pytest.mark.parametrize("pattern", PATTERNS)
+def test_fused_matches_oracle(cuda, oracle, moe, batch, pattern):
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16
+    flat = oracle.moe_patterns(batch, random.Random(37))[pattern]
+    ids = torch.tensor(flat, dtype=torch.int32, device=cuda).view(batch, 8)
+    g = torch.Generator(device=cuda).manual_seed(1000 * batch + PATTERNS.index(pattern))
+    x, _, tw = W.moe_w4a16_inputs(batch, cuda, g, ids=ids)
+    d = moe["dev"]
+    log_case("fused moe", batch, pattern)
+    out = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids)
+    torch.cuda.synchronize()
+    want, _ = run_oracle(oracle, moe, x, ids, tw)
+    assert_out_close(out, want, oracle, f"B={batch} {pattern}")
+    if pattern == "all_invalid":
+        assert not out.float().abs().sum().item()
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_gate_up_activation_matches_oracle(cuda, oracle, moe, batch):
+    """The first kernel alone, fed by the aligner: c2 of every routed slot."""
+    import torch
+    from titan_moe_align import titan_moe_align_small
+    from titan_moe_w4a16 import moe_w4a16_gate_up, moe_w4a16_down
+    g = torch.Generator(device=cuda).manual_seed(77 + batch)
+    x, ids, tw = W.moe_w4a16_inputs(batch, cuda, g)
+    ids[0, :3] = ids[0, 4]                      # a shared expert: an aligner block with several slots
+    d = moe["dev"]
+    log_case("gate_up + down", batch)
+    sorted_ids, expert_ids, _ = titan_moe_align_small(ids)
+    act = moe_w4a16_gate_up(x, d["w13"], d["w13_scale"], sorted_ids, expert_ids)
+    out = moe_w4a16_down(act, d["w2"], d["w2_scale"], tw, ids)
+    torch.cuda.synchronize()
+    want_out, want_act = run_oracle(oracle, moe, x, ids, tw)
+    assert_act_close(act, want_act, np.arange(batch * 8), oracle, f"B={batch} c2")
+    assert_out_close(out, want_out, oracle, f"B={batch} out")
+
+
+def test_int64_ids_and_invalid_routes(cuda, oracle, moe):
+    """int64 ids are compared at full width (5 + 2^32 is not expert 5) and
+    every route outside [0, 288) contributes exactly nothing."""
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16
+    g = torch.Generator(device=cuda).manual_seed(91)
+    x, ids, tw = W.moe_w4a16_inputs(4, cuda, g)
+    ids64 = ids.to(torch.int64)
+    ids64[0, 1] = 5 + 2 ** 32
+    ids64[1, 0] = -1
+    ids64[2, 7] = 288
+    ids64[3, 3] = -(2 ** 40)
+    d = moe["dev"]
+    log_case("fused moe int64 ids with invalid routes")
+    out = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids64)
+    tw0 = tw.clone()
+    for t, j in ((0, 1), (1, 0), (2, 7), (3, 3)):
+        tw0[t, j] = 0
+    ids_ok = torch.where((ids64 >= 0) & (ids64 < 288), ids64, torch.zeros_like(ids64)).to(torch.int32)
+    ref = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw0, ids_ok.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    want, _ = run_oracle(oracle, moe, x, ids64, tw)
+    assert_out_close(out, want, oracle, "int64 invalid")
+
+
+def test_clamp_off_row_stride_and_output(cuda, oracle, moe):
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16
+    g = torch.Generator(device=cuda).manual_seed(92)
+    big = (3.0 * torch.randn(3, 4096 + 64, generator=g, device=cuda)).to(torch.bfloat16)
+    x = big[:, 32:32 + 4096]                      # row stride 4160 elements, 64-byte aligned start
+    _, ids, tw = W.moe_w4a16_inputs(3, cuda, g)
+    d = moe["dev"]
+    out = torch.full((3, 4096), 7.0, dtype=torch.bfloat16, device=cuda)
+    log_case("fused moe, clamp off, strided rows, output=")
+    ret = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids, clamp_limit=None,
+                          output=out)
+    assert ret.data_ptr() == out.data_ptr()
+    clamped = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids)
+    torch.cuda.synchronize()
+    want, _ = run_oracle(oracle, moe, x, ids, tw, clamp=None)
+    assert_out_close(out, want, oracle, "clamp off")
+    want_c, _ = run_oracle(oracle, moe, x, ids, tw, clamp=10.0)
+    assert_out_close(clamped, want_c, oracle, "clamp 10")
+    assert not torch.equal(out, clamped)          # 3-sigma inputs push gate/up past 10
+
+
+def test_graph_replay_deterministic(cuda, moe):
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16
+    g = torch.Generator(device=cuda).manual_seed(93)
+    x, ids, tw = W.moe_w4a16_inputs(8, cuda, g)
+    d = moe["dev"]
+    fn = lambda: fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids)
+    log_case("fused moe graph capture B=8")
+    eager = fn()
+    again = fn()
+    torch.cuda.synchronize()
+    assert torch.equal(eager, again)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = fn()
+    for i in range(4):
+        captured.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), f"replay {i}"
+        fn()                                          # eager work between replays
+        torch.cuda.synchronize()

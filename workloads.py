@@ -168,6 +168,55 @@ def moe_routes(batch, device, g, dtype=torch.int32):
     return keys.argsort(dim=1)[:, :8].to(dtype).contiguous()
 
 
+# ----------------------------------------------------------------- MoE W4A16 layer
+
+MOE_EXPERTS = 288
+MOE_HIDDEN = 4096
+MOE_INTER = 512      # per-rank expert intermediate size under TP4
+MOE_TOPK = 8
+
+
+def moe_w4a16_layer(device, seed=SEED_BENCH, experts=MOE_EXPERTS, hidden=MOE_HIDDEN, inter=MOE_INTER):
+    """Random-init W4A16 group-32 expert weights at the GLM-5.3 TP4 shape in
+    the checkpoint packing (int32 [E, n_out, K/8], bf16 scales [E, n_out,
+    K/32]): uniform 4-bit codes (std of q - 8 = 4.61) and scales drawn around
+    1 / (4.61 sqrt(K)) for W13 and 1 / (0.6 * 4.61 sqrt(N)) for W2, so gate,
+    up and the down outputs have unit scale for unit-normal inputs."""
+    g = gen(device, seed)
+    codes = lambda n_out, k: torch.randint(0, 256, (experts, n_out, k // 2), generator=g, device=device,
+                                           dtype=torch.uint8).view(torch.int32)
+    scale = lambda n_out, k, base: ((torch.rand(experts, n_out, k // 32, generator=g, device=device) + 0.5)
+                                    * base).to(torch.bfloat16)
+    return {
+        "w13_packed": codes(2 * inter, hidden),
+        "w13_scale": scale(2 * inter, hidden, 1.0 / (4.61 * math.sqrt(hidden))),
+        "w2_packed": codes(hidden, inter),
+        "w2_scale": scale(hidden, inter, 1.0 / (0.6 * 4.61 * math.sqrt(inter))),
+    }
+
+
+def moe_w4a16_inputs(batch, device, g, hidden=MOE_HIDDEN, ids=None):
+    """Decode tokens for the MoE layer: unit-normal bf16 hidden states, 8
+    distinct experts per token (unless ids are given) and softmax router
+    weights (fp32, each row sums to 1)."""
+    x = torch.randn(batch, hidden, generator=g, device=device).to(torch.bfloat16)
+    if ids is None:
+        ids = moe_routes(batch, device, g)
+    logits = torch.randn(batch, MOE_TOPK, generator=g, device=device)
+    return x, ids, torch.softmax(logits, dim=1).contiguous()
+
+
+def moe_w4a16_bytes(ids: torch.Tensor, batch: int, experts=MOE_EXPERTS, hidden=MOE_HIDDEN,
+                    inter=MOE_INTER) -> int:
+    """Algorithmic bytes of one MoE layer call: the codes and scales of
+    every distinct expert the routes use (W13 and W2), the hidden states in
+    and the output out.  The c2 intermediate is implementation traffic."""
+    e = ids.flatten().long()
+    distinct = int(torch.unique(e[(e >= 0) & (e < experts)]).numel())
+    per_expert = (2 * inter * hidden + hidden * inter) // 2 + (2 * inter * hidden + hidden * inter) // 32 * 2
+    return distinct * per_expert + 2 * batch * hidden * 2
+
+
 # ----------------------------------------------------------------- bytes
 
 def writer_bytes(n_rows: int) -> int:
