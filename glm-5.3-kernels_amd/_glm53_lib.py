@@ -79,7 +79,7 @@ def load():
     L.glm53_moe_align_small.argtypes = [P, I, I64, P, P, P, P]
     F = ctypes.c_float
     L.glm53_moe_w4a16_repack.restype = I
-    L.glm53_moe_w4a16_repack.argtypes = [P, I64, I64, I64, P, P]
+    L.glm53_moe_w4a16_repack.argtypes = [P, P, I64, I64, I64, P, P, P]
     L.glm53_moe_w4a16_gate_up.restype = I
     L.glm53_moe_w4a16_gate_up.argtypes = [P, I64, P, P, P, P, I64, I64, I64, I64, I64, F, P, P]
     L.glm53_moe_w4a16_down.restype = I

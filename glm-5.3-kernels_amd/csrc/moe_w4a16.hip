@@ -19,8 +19,11 @@
 // [0, 8) for the tile's 128-feature chunk c, with k = 2j in bits 4j and k =
 // 2j + 1 in bits 16 + 4j.  So a 16-byte load per lane brings four groups of
 // the MFMA's B operand, and (word >> 4j) & 0x000F000F | 0x43004300 is the
-// bf16 pair (128 + q_2j, 128 + q_2j+1) with two VALU ops.  Scales stay in the
-// checkpoint's [E][n_out][K/32] bf16 layout.
+// bf16 pair (128 + q_2j, 128 + q_2j+1) with two VALU ops.  The checkpoint's
+// bf16 scales [E][n_out][K/32] are reordered the same way, [E][n_out/16]
+// [K/128][16 rows][4 groups]: a lane's four scales of a chunk are 8 bytes and
+// the 16 rows of a tile's chunk one 128-byte line (row-major scales put the
+// 16 rows 256 bytes apart, sixteen lines per load instruction).
 //
 // Per group of 32 features, D[m][n] = X[m][32] . B[32][n] runs on
 // v_mfma_f32_16x16x32_bf16 with A = the activation rows (m = route slot) and
@@ -37,7 +40,7 @@
 // Down kernel: one workgroup per (token, 16 output features); wavefront j
 // computes route slot j of the token (its expert's 16 rows over N), the 8
 // weighted results are summed in slot order.  Both kernels are deterministic.
-#include "glm53_common.h"
+#include "moe_route.h"
 
 namespace glm53 {
 namespace {
@@ -79,9 +82,10 @@ __device__ __forceinline__ float bf16_round(float f) { return bf16_bits_to_f32(f
 
 // ------------------------------------------------------------------ repack
 __global__ __launch_bounds__(256) void moe_w4a16_repack_kernel(const uint32_t* __restrict__ src,
+                                                               const uint16_t* __restrict__ src_s,
                                                                uint32_t* __restrict__ dst,
-                                                               int64_t total_words, int n_tiles,
-                                                               int k_chunks, int k_words) {
+                                                               uint16_t* __restrict__ dst_s,
+                                                               int64_t total_words, int k_chunks) {
   const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (d >= total_words) return;
   const int i = static_cast<int>(d & 3);
@@ -90,6 +94,7 @@ __global__ __launch_bounds__(256) void moe_w4a16_repack_kernel(const uint32_t* _
   const int c = static_cast<int>(rest % k_chunks);
   const int64_t et = rest / k_chunks;           // e * n_tiles + tile
   const int64_t row = et * kTileN + (l & 15);   // e * n_out + n
+  const int k_words = 16 * k_chunks;
   const uint32_t w = src[row * k_words + 4 * (4 * c + i) + (l >> 4)];
   uint32_t o = 0;
 #pragma unroll
@@ -98,19 +103,28 @@ __global__ __launch_bounds__(256) void moe_w4a16_repack_kernel(const uint32_t* _
     o |= ((w >> (8 * j + 4)) & 0xFu) << (16 + 4 * j);   // k = 2j + 1
   }
   dst[d] = o;
-  (void)n_tiles;
+  if (l < kTileN)   // scale of row l, group 4c + i
+    dst_s[rest * 64 + 4 * l + i] = src_s[row * (4 * k_chunks) + 4 * c + i];
 }
 
 // ------------------------------------------------------------------ gate/up
+constexpr int kMaxHidden = 4096;          // activation rows staged in LDS
+constexpr int kXStride = kMaxHidden + 8;  // 16-byte pad: the 8 rows start 4 banks apart
+constexpr int kMaxInter = 2048;           // c2 rows staged in LDS by the down kernel
+constexpr int kActStride = kMaxInter + 8;
+
 struct GateUpArgs {
   const uint16_t* x;        // bf16 [T][K], row stride sx (elements)
   int64_t sx;
   const uint4* w13;         // repacked [E][2N/16][K/128][64] uint4
-  const uint16_t* s13;      // bf16 [E][2N][K/32]
-  const int32_t* sorted_ids;
+  const uint16_t* s13;      // bf16 scales in tile order [E][2N/16][K/128][16][4]
+  const int32_t* sorted_ids;  // aligner outputs (kSelfAlign = false)
   const int32_t* expert_ids;
-  int num_routes;           // R = T * topk (padding value in sorted_ids)
+  const void* topk_ids;     // contiguous [T * topk] routes (kSelfAlign = true)
+  int ids_i64;
+  int num_routes;           // R = T * topk (padding value of sorted_ids)
   int topk;
+  int topk_log2;            // log2(topk) when topk is a power of two, else -1
   int num_experts;
   int n_inter;              // N
   int hidden;               // K
@@ -118,84 +132,131 @@ struct GateUpArgs {
   uint16_t* act;            // bf16 [R][N]
 };
 
-struct GateUpShared {
-  float red[kWaves][2][4][64];
+union __align__(16) GateUpShared {
+  uint16_t x[kBlock][kXStride];            // the block's activation rows
+  float red[kWaves][2][4][64];             // partial tiles, after the last x read
 };
 
+// The MFMA loop over this wave's chunks of a gate tile and an up tile.
+// kSingle: only D row 0 (slot 0) is kept, so one scale FMA per group and tile
+// instead of four.
+template <bool kSingle>
+__device__ __forceinline__ void gate_up_chunks(const uint16_t* xs, int c_lo, int cpw, int k_chunks,
+                                               const uint4 (&kg)[kBatch], const uint4 (&ku)[kBatch],
+                                               const uint2 (&scg)[kBatch], const uint2 (&scu)[kBatch],
+                                               f32x4& acc_g, f32x4& acc_u) {
+  const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
+  const uint32_t mask = nibble_mask();
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {
+    const int c = c_lo + u;
+    if (u >= cpw || c >= k_chunks) break;   // uniform
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(xs + kChunkK * c + kGroup * i);
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
+      const f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(kg[u], i), mask), corr, 0, 0, 0);
+      const f32x4 du = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ku[u], i), mask), corr, 0, 0, 0);
+      const uint32_t pg = i < 2 ? scg[u].x : scg[u].y;
+      const uint32_t pu = i < 2 ? scu[u].x : scu[u].y;
+      const float s_g = __uint_as_float((i & 1) ? (pg & 0xFFFF0000u) : (pg << 16));
+      const float s_u = __uint_as_float((i & 1) ? (pu & 0xFFFF0000u) : (pu << 16));
+#pragma unroll
+      for (int r = 0; r < (kSingle ? 1 : 4); r++) {
+        acc_g[r] = __builtin_fmaf(s_g, dg[r], acc_g[r]);
+        acc_u[r] = __builtin_fmaf(s_u, du[r], acc_u[r]);
+      }
+    }
+  }
+}
+
+// kSelfAlign: the workgroup derives its aligner block (expert and 8 slots)
+// from the routes itself, with the aligner's ballots, instead of loading
+// sorted_ids / expert_ids: one launch and one dependent load fewer.
+template <bool kSelfAlign>
 __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateUpArgs a) {
   __shared__ GateUpShared sh;
   const int b = blockIdx.x;
   const int jt = blockIdx.y;
-  const int e = a.expert_ids[b];
-  if (e < 0 || e >= a.num_experts) return;   // unused aligner block (uniform)
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   const int q = lane >> 4, col = lane & 15;
+  const int R = a.num_routes;
 
-  // Route slot of this lane's A rows (m = col) and whether it holds a route.
-  const int sid = a.sorted_ids[kBlock * b + (col & 7)];
-  const bool row_ok = col < kBlock && sid < a.num_routes;
-  const uint16_t* xrow = a.x + static_cast<int64_t>(row_ok ? sid / a.topk : 0) * a.sx + 8 * q;
-
-  const int k_chunks = a.hidden / kChunkK;
-  const int k_groups = a.hidden / kGroup;
-  const int n_tiles13 = 2 * a.n_inter / kTileN;
-  const uint4* wg = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + jt) * k_chunks) * 64 + lane;
-  const uint4* wu = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + a.n_inter / kTileN + jt) * k_chunks) * 64 + lane;
-  const int ng = kTileN * jt + col;
-  const uint16_t* sg = a.s13 + (static_cast<int64_t>(e) * 2 * a.n_inter + ng) * k_groups;
-  const uint16_t* su = sg + static_cast<int64_t>(a.n_inter) * k_groups;
-
-  const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
-  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
-  const uint32_t mask = nibble_mask();
-
-  for (int c0 = w; c0 < k_chunks; c0 += kWaves * kBatch) {
-    uint4 kg[kBatch], ku[kBatch];
-    uint2 scg[kBatch], scu[kBatch];
-    uint4 xa[kBatch][4];
+  int slot[kBlock];   // route of each slot of the block (R = padding); wave-uniform
+  int e;
+  if (kSelfAlign) {
+    const bool in = lane < R;
+    const RoutePos rp = align_routes(in ? load_route_id(a.topk_ids, a.ids_i64, lane) : -1, in);
 #pragma unroll
-    for (int u = 0; u < kBatch; u++) {
-      const int c = c0 + kWaves * u;
-      kg[u] = ku[u] = make_uint4(0, 0, 0, 0);
-      scg[u] = scu[u] = make_uint2(0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; i++) xa[u][i] = make_uint4(0, 0, 0, 0);
-      if (c < k_chunks) {
-        kg[u] = wg[static_cast<int64_t>(c) * 64];
-        ku[u] = wu[static_cast<int64_t>(c) * 64];
-        scg[u] = *reinterpret_cast<const uint2*>(sg + 4 * c);
-        scu[u] = *reinterpret_cast<const uint2*>(su + 4 * c);
-        if (row_ok) {
-#pragma unroll
-          for (int i = 0; i < 4; i++)
-            xa[u][i] = *reinterpret_cast<const uint4*>(xrow + kChunkK * c + kGroup * i);
-        }
-      }
+    for (int m = 0; m < kBlock; m++) {
+      const uint64_t hit = __ballot(rp.valid && rp.pos == kBlock * b + m);
+      slot[m] = hit ? __builtin_ctzll(hit) : R;
     }
+    e = slot[0] < R ? __builtin_amdgcn_readlane(rp.key, slot[0]) : -1;
+  } else {
+    e = a.expert_ids[b];
 #pragma unroll
-    for (int u = 0; u < kBatch; u++) {
-      if (c0 + kWaves * u >= k_chunks) break;   // uniform
+    for (int m = 0; m < kBlock; m++) slot[m] = a.sorted_ids[kBlock * b + m];
+  }
+  if (e < 0 || e >= a.num_experts) return;   // unused block (uniform over the workgroup)
+
+  // Wave w owns chunks [cpw*w, cpw*w + cpw) of K (cpw <= kBatch).  It stages
+  // the block's activation rows over that range into LDS with direct
+  // global->LDS loads (lane i -> 16 bytes at i*16; no VGPRs), so the MFMA
+  // loop reads only what this wave loaded and needs no workgroup barrier.
+  const int k_chunks = a.hidden / kChunkK;
+  const int cpw = (k_chunks + kWaves - 1) / kWaves;
+  const int c_lo = cpw * w;
+  const int kbase = kChunkK * c_lo;                 // first feature of this wave
+  const bool x_lane = 8 * lane < kChunkK * cpw && kbase + 8 * lane < a.hidden;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const bf16x8 xv = __builtin_bit_cast(bf16x8, xa[u][i]);
-        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
-        const f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(kg[u], i), mask), corr, 0, 0, 0);
-        const f32x4 du = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ku[u], i), mask), corr, 0, 0, 0);
-        const uint32_t pg = i < 2 ? scg[u].x : scg[u].y;
-        const uint32_t pu = i < 2 ? scu[u].x : scu[u].y;
-        const float s_g = __uint_as_float((i & 1) ? (pg & 0xFFFF0000u) : (pg << 16));
-        const float s_u = __uint_as_float((i & 1) ? (pu & 0xFFFF0000u) : (pu << 16));
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          acc_g[r] = __builtin_fmaf(s_g, dg[r], acc_g[r]);
-          acc_u[r] = __builtin_fmaf(s_u, du[r], acc_u[r]);
-        }
-      }
+  for (int m = 0; m < kBlock; m++) {
+    if (slot[m] < R && x_lane) {
+      const unsigned route = static_cast<unsigned>(slot[m]);
+      const unsigned tok = a.topk_log2 >= 0 ? route >> a.topk_log2 : route / static_cast<unsigned>(a.topk);
+      __builtin_amdgcn_global_load_lds(a.x + static_cast<int64_t>(tok) * a.sx + kbase + 8 * lane,
+                                       &sh.x[m][kbase], 16, 0, 0);
     }
   }
 
+  // This wave's chunks of the gate and up tiles and their scales.
+  const int n_tiles13 = 2 * a.n_inter / kTileN;
+  const uint4* wg = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + jt) * k_chunks) * 64 + lane;
+  const uint4* wu = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + a.n_inter / kTileN + jt) * k_chunks) * 64 + lane;
+  const uint16_t* sg = a.s13 + ((static_cast<int64_t>(e) * n_tiles13 + jt) * k_chunks) * 64 + 4 * col;
+  const uint16_t* su = a.s13 + ((static_cast<int64_t>(e) * n_tiles13 + a.n_inter / kTileN + jt) * k_chunks) * 64 + 4 * col;
+  uint4 kg[kBatch], ku[kBatch];
+  uint2 scg[kBatch], scu[kBatch];
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {   // chunks past the wave's range re-read its last one (not used)
+    const int c = c_lo + (u < cpw ? u : cpw - 1) < k_chunks ? c_lo + (u < cpw ? u : cpw - 1) : k_chunks - 1;
+    kg[u] = wg[static_cast<int64_t>(c) * 64];
+    ku[u] = wu[static_cast<int64_t>(c) * 64];
+    scg[u] = *reinterpret_cast<const uint2*>(sg + 64 * c);
+    scu[u] = *reinterpret_cast<const uint2*>(su + 64 * c);
+  }
+
+  // A-operand row of this lane (m = col): padding slots and m >= 8 read row 0
+  // (their D rows are discarded), so a block with one route reads one row.
+  int xrow = 0;
+#pragma unroll
+  for (int m = 1; m < kBlock; m++)
+    if ((col & 7) == m && slot[m] < R) xrow = m;
+  const uint16_t* xs = &sh.x[xrow][8 * q];
+
+  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's staged rows are in LDS
+  bool single = true;                   // only slot 0 routed: D row 0 is the only one kept
+#pragma unroll
+  for (int m = 1; m < kBlock; m++) single = single && slot[m] >= R;
+  if (single)
+    gate_up_chunks<true>(xs, c_lo, cpw, k_chunks, kg, ku, scg, scu, acc_g, acc_u);
+  else
+    gate_up_chunks<false>(xs, c_lo, cpw, k_chunks, kg, ku, scg, scu, acc_g, acc_u);
+
+  __syncthreads();   // every wave is done with x: red reuses its space
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     sh.red[w][0][r][lane] = acc_g[r];
@@ -204,9 +265,12 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
   __syncthreads();
   if (threadIdx.x < kTileN * kBlock) {
     const int n = threadIdx.x & 15;
-    const int m = threadIdx.x >> 4;   // route slot 0..7: lane n + 16*(m/4), element m%4
-    const int slot = a.sorted_ids[kBlock * b + m];
-    if (slot < a.num_routes) {
+    const int m = threadIdx.x >> 4;   // slot 0..7: D row m sits in lane n + 16*(m/4), element m%4
+    int route = R;
+#pragma unroll
+    for (int mm = 0; mm < kBlock; mm++)
+      if (m == mm) route = slot[mm];
+    if (route < R) {
       float g = 0.f, up = 0.f;
 #pragma unroll
       for (int ww = 0; ww < kWaves; ww++) {
@@ -216,7 +280,7 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
       g = fminf(bf16_round(g), a.clamp);
       up = fminf(fmaxf(bf16_round(up), -a.clamp), a.clamp);
       const float v = g / (1.0f + expf(-g)) * up;
-      a.act[static_cast<int64_t>(slot) * a.n_inter + kTileN * jt + n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+      a.act[static_cast<int64_t>(route) * a.n_inter + kTileN * jt + n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
     }
   }
 }
@@ -225,7 +289,7 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
 struct DownArgs {
   const uint16_t* act;      // bf16 [T * topk][N]
   const uint4* w2;          // repacked [E][K/16][N/128][64] uint4
-  const uint16_t* s2;       // bf16 [E][K][N/32]
+  const uint16_t* s2;       // bf16 scales in tile order [E][K/16][N/128][16][4]
   const void* topk_ids;     // [T][topk] int32 / int64, row stride sid_t
   int ids_i64;
   int64_t sid_t;
@@ -239,76 +303,86 @@ struct DownArgs {
   int64_t so;
 };
 
+// Weight words and scales of chunks [c0, c0 + kBatch) of a down tile.
+__device__ __forceinline__ void load_down_batch(const uint4* wp, const uint16_t* sp, int c0, int k_chunks,
+                                                uint4 (&kw)[kBatch], uint2 (&sc)[kBatch]) {
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {   // chunks past N re-read the last one (not used)
+    const int c = c0 + u < k_chunks ? c0 + u : k_chunks - 1;
+    kw[u] = wp[static_cast<int64_t>(c) * 64];
+    sc[u] = *reinterpret_cast<const uint2*>(sp + 64 * c);
+  }
+}
+
+struct __align__(16) DownShared {
+  uint16_t act[kWaves][kActStride];   // the token's c2 rows
+  float part[kWaves][kTileN];
+};
+
 __global__ __launch_bounds__(kThreads) void moe_w4a16_down_kernel(const DownArgs a) {
-  __shared__ float part[kWaves][kTileN];
+  __shared__ DownShared sh;
   const int nt = blockIdx.x;
   const int t = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   const int q = lane >> 4, col = lane & 15;
   const int k_chunks = a.n_inter / kChunkK;
-  const int k_groups = a.n_inter / kGroup;
   const int n_tiles2 = a.hidden / kTileN;
-  const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
-  const uint32_t mask = nibble_mask();
+  const bool has_route = w < a.topk;   // wave w computes route slot w (topk <= 8)
 
-  for (int j = w; j < a.topk; j += kWaves) {
-    int64_t raw = a.ids_i64 ? static_cast<const int64_t*>(a.topk_ids)[t * a.sid_t + j]
-                            : static_cast<int64_t>(static_cast<const int32_t*>(a.topk_ids)[t * a.sid_t + j]);
-    const bool ok = uniform(raw >= 0 && raw < a.num_experts);   // the same id in every lane
-    float y = 0.f;
-    if (ok) {
-      const int e = uniform(static_cast<int>(raw));
-      const uint4* wp = a.w2 + ((static_cast<int64_t>(e) * n_tiles2 + nt) * k_chunks) * 64 + lane;
-      const uint16_t* sp = a.s2 + (static_cast<int64_t>(e) * a.hidden + kTileN * nt + col) * k_groups;
-      const uint16_t* ar = a.act + (static_cast<int64_t>(t) * a.topk + j) * a.n_inter + 8 * q;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int c0 = 0; c0 < k_chunks; c0 += kBatch) {
-        uint4 kw[kBatch];
-        uint2 sc[kBatch];
-        uint4 xa[kBatch][4];
+  // Route of this wave (the same id in every lane).
+  int e = -1;
+  if (has_route) {
+    const int64_t raw = load_route_id(a.topk_ids, a.ids_i64, static_cast<int>(t * a.sid_t + w));
+    e = uniform(raw >= 0 && raw < a.num_experts ? static_cast<int>(raw) : -1);
+  }
+  const uint4* wp = a.w2 + ((static_cast<int64_t>(e < 0 ? 0 : e) * n_tiles2 + nt) * k_chunks) * 64 + lane;
+  const uint16_t* sp = a.s2 + ((static_cast<int64_t>(e < 0 ? 0 : e) * n_tiles2 + nt) * k_chunks) * 64 + 4 * col;
+  // The wave's own c2 row into LDS with direct global->LDS loads (lane i ->
+  // 16 bytes at i*16), then the first weight batch; only this wave reads the
+  // row, so no workgroup barrier is needed before the MFMA loop.
+  const uint16_t* act_r = a.act + (static_cast<int64_t>(t) * a.topk + w) * a.n_inter;
+  if (e >= 0) {
+    for (int k0 = 0; k0 < a.n_inter; k0 += 8 * 64)
+      if (k0 + 8 * lane < a.n_inter)
+        __builtin_amdgcn_global_load_lds(act_r + k0 + 8 * lane, &sh.act[w][k0], 16, 0, 0);
+  }
+  uint4 kw[kBatch];
+  uint2 sc[kBatch];
+  if (e >= 0) load_down_batch(wp, sp, 0, k_chunks, kw, sc);
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): the staged row is in LDS
+
+  float y = 0.f;
+  if (e >= 0) {
+    const uint16_t* xs = &sh.act[w][8 * q];   // D row 0 is the route; the other rows repeat it
+    const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
+    const uint32_t mask = nibble_mask();
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < k_chunks; c0 += kBatch) {
+      if (c0 > 0) load_down_batch(wp, sp, c0, k_chunks, kw, sc);
 #pragma unroll
-        for (int u = 0; u < kBatch; u++) {
-          const int c = c0 + u;
-          kw[u] = make_uint4(0, 0, 0, 0);
-          sc[u] = make_uint2(0, 0);
+      for (int u = 0; u < kBatch; u++) {
+        const int c = c0 + u;
+        if (c >= k_chunks) break;
 #pragma unroll
-          for (int i = 0; i < 4; i++) xa[u][i] = make_uint4(0, 0, 0, 0);
-          if (c < k_chunks) {
-            kw[u] = wp[static_cast<int64_t>(c) * 64];
-            sc[u] = *reinterpret_cast<const uint2*>(sp + 4 * c);
-            if (col == 0) {
-#pragma unroll
-              for (int i = 0; i < 4; i++)
-                xa[u][i] = *reinterpret_cast<const uint4*>(ar + kChunkK * c + kGroup * i);
-            }
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < kBatch; u++) {
-          if (c0 + u >= k_chunks) break;
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const bf16x8 xv = __builtin_bit_cast(bf16x8, xa[u][i]);
-            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
-            const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(kw[u], i), mask), corr, 0, 0, 0);
-            const uint32_t p = i < 2 ? sc[u].x : sc[u].y;
-            const float s = __uint_as_float((i & 1) ? (p & 0xFFFF0000u) : (p << 16));
-            acc[0] = __builtin_fmaf(s, d[0], acc[0]);   // row m = 0: lanes 0..15, element 0
-          }
+        for (int i = 0; i < 4; i++) {
+          const bf16x8 xv = *reinterpret_cast<const bf16x8*>(xs + kChunkK * c + kGroup * i);
+          const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+          const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
+          const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(kw[u], i), mask), corr, 0, 0, 0);
+          const uint32_t p = i < 2 ? sc[u].x : sc[u].y;
+          const float s = __uint_as_float((i & 1) ? (p & 0xFFFF0000u) : (p << 16));
+          acc[0] = __builtin_fmaf(s, d[0], acc[0]);   // D row 0: lanes 0..15, element 0
         }
       }
-      const float tw = a.topk_w[t * a.sw_t + j];
-      y = bf16_round(tw * acc[0]);
     }
-    if (lane < kTileN) part[w][lane] = y;
+    y = bf16_round(a.topk_w[t * a.sw_t + w] * acc[0]);
   }
+  if (has_route && lane < kTileN) sh.part[w][lane] = y;
   __syncthreads();
   if (threadIdx.x < kTileN) {
     float s = 0.f;
-    const int nw = a.topk < kWaves ? a.topk : kWaves;
-    for (int ww = 0; ww < nw; ww++) s += part[ww][threadIdx.x];
+    for (int ww = 0; ww < a.topk; ww++) s += sh.part[ww][threadIdx.x];
     a.out[t * a.so + kTileN * nt + threadIdx.x] = static_cast<uint16_t>(f32_to_bf16_bits(s));
   }
 }
@@ -320,44 +394,61 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 using namespace glm53;
 
-extern "C" int glm53_moe_align_small(const void* topk_ids, int ids_is_i64, int64_t num_routes,
-                                     int32_t* sorted_ids, int32_t* expert_ids,
-                                     int32_t* num_tokens_post_padded, void* stream);
-
-extern "C" int glm53_moe_w4a16_repack(const void* w_packed, int64_t num_experts, int64_t n_out,
-                                      int64_t k, void* out, void* stream) {
-  if (!w_packed || !out) return GLM53_ERR_NULL_POINTER;
+extern "C" int glm53_moe_w4a16_repack(const void* w_packed, const void* w_scale, int64_t num_experts,
+                                      int64_t n_out, int64_t k, void* out, void* out_scale, void* stream) {
+  if (!w_packed || !w_scale || !out || !out_scale) return GLM53_ERR_NULL_POINTER;
   if (num_experts < 1 || n_out < kTileN || n_out % kTileN || k < kChunkK || k % kChunkK)
     return GLM53_ERR_BAD_SHAPE;
-  if (!aligned16(out) || (reinterpret_cast<uintptr_t>(w_packed) & 3)) return GLM53_ERR_MISALIGNED;
+  if (!aligned16(out) || (reinterpret_cast<uintptr_t>(w_packed) & 3) || (reinterpret_cast<uintptr_t>(w_scale) & 1) ||
+      (reinterpret_cast<uintptr_t>(out_scale) & 7))
+    return GLM53_ERR_MISALIGNED;
   const int64_t total = num_experts * n_out * (k / 8);
   (void)hipGetLastError();
   hipLaunchKernelGGL(moe_w4a16_repack_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint32_t*>(w_packed),
-                     static_cast<uint32_t*>(out), total, static_cast<int>(n_out / kTileN),
-                     static_cast<int>(k / kChunkK), static_cast<int>(k / 8));
+                     static_cast<const uint16_t*>(w_scale), static_cast<uint32_t*>(out),
+                     static_cast<uint16_t*>(out_scale), total, static_cast<int>(k / kChunkK));
   return static_cast<int>(hipGetLastError());
 }
+
+namespace {
+
+int launch_gate_up(bool self_align, const void* x, int64_t sx, const void* w13, const void* s13,
+                   const int32_t* sorted_ids, const int32_t* expert_ids, const void* topk_ids, int ids_is_i64,
+                   int64_t num_routes, int64_t topk, int64_t num_experts, int64_t n_inter, int64_t hidden,
+                   float clamp_limit, void* act, void* stream) {
+  if (!x || !w13 || !s13 || !act) return GLM53_ERR_NULL_POINTER;
+  if (self_align ? !topk_ids : (!sorted_ids || !expert_ids)) return GLM53_ERR_NULL_POINTER;
+  if (num_routes < 1 || num_routes > (self_align ? kAlignMaxRoutes : (1 << 24)) || topk < 1 || num_experts < 1 ||
+      n_inter < kTileN || n_inter % kTileN || hidden < kChunkK || hidden % kChunkK || hidden > kMaxHidden ||
+      sx < hidden || !(clamp_limit > 0.f))
+    return GLM53_ERR_BAD_SHAPE;
+  if (!aligned16(x) || sx % 8 || !aligned16(w13) || (reinterpret_cast<uintptr_t>(s13) & 7) ||
+      (reinterpret_cast<uintptr_t>(act) & 1))
+    return GLM53_ERR_MISALIGNED;
+  GateUpArgs a{static_cast<const uint16_t*>(x), sx, static_cast<const uint4*>(w13),
+               static_cast<const uint16_t*>(s13), sorted_ids, expert_ids, topk_ids, ids_is_i64,
+               static_cast<int>(num_routes), static_cast<int>(topk),
+               (topk & (topk - 1)) ? -1 : __builtin_ctzll(static_cast<uint64_t>(topk)), static_cast<int>(num_experts),
+               static_cast<int>(n_inter), static_cast<int>(hidden), clamp_limit, static_cast<uint16_t*>(act)};
+  const dim3 grid(static_cast<unsigned>(num_routes), static_cast<unsigned>(n_inter / kTileN));
+  (void)hipGetLastError();
+  if (self_align)
+    hipLaunchKernelGGL(moe_w4a16_gate_up_kernel<true>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(moe_w4a16_gate_up_kernel<false>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
 
 extern "C" int glm53_moe_w4a16_gate_up(const void* x, int64_t sx, const void* w13, const void* s13,
                                        const int32_t* sorted_ids, const int32_t* expert_ids,
                                        int64_t num_routes, int64_t topk, int64_t num_experts,
                                        int64_t n_inter, int64_t hidden, float clamp_limit, void* act,
                                        void* stream) {
-  if (!x || !w13 || !s13 || !sorted_ids || !expert_ids || !act) return GLM53_ERR_NULL_POINTER;
-  if (num_routes < 1 || num_routes > (1 << 24) || topk < 1 || num_experts < 1 || n_inter < kTileN ||
-      n_inter % kTileN || hidden < kChunkK || hidden % kChunkK || sx < hidden || !(clamp_limit > 0.f))
-    return GLM53_ERR_BAD_SHAPE;
-  if (!aligned16(x) || sx % 8 || !aligned16(w13) || (reinterpret_cast<uintptr_t>(s13) & 7) || (reinterpret_cast<uintptr_t>(act) & 1))
-    return GLM53_ERR_MISALIGNED;
-  GateUpArgs a{static_cast<const uint16_t*>(x), sx, static_cast<const uint4*>(w13),
-               static_cast<const uint16_t*>(s13), sorted_ids, expert_ids, static_cast<int>(num_routes),
-               static_cast<int>(topk), static_cast<int>(num_experts), static_cast<int>(n_inter),
-               static_cast<int>(hidden), clamp_limit, static_cast<uint16_t*>(act)};
-  (void)hipGetLastError();
-  hipLaunchKernelGGL(moe_w4a16_gate_up_kernel, dim3(static_cast<unsigned>(num_routes), static_cast<unsigned>(n_inter / kTileN)),
-                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
-  return static_cast<int>(hipGetLastError());
+  return launch_gate_up(false, x, sx, w13, s13, sorted_ids, expert_ids, nullptr, 0, num_routes, topk, num_experts,
+                        n_inter, hidden, clamp_limit, act, stream);
 }
 
 extern "C" int glm53_moe_w4a16_down(const void* act, const void* w2, const void* s2, const void* topk_ids,
@@ -366,8 +457,8 @@ extern "C" int glm53_moe_w4a16_down(const void* act, const void* w2, const void*
                                     int64_t hidden, void* out, int64_t so, void* stream) {
   if (!act || !w2 || !s2 || !topk_ids || !topk_weights || !out) return GLM53_ERR_NULL_POINTER;
   if (num_tokens < 1 || num_tokens > 65535 || topk < 1 || topk > kWaves || num_experts < 1 ||
-      n_inter < kChunkK || n_inter % kChunkK || hidden < kTileN || hidden % kTileN || sid_t < topk ||
-      sw_t < topk || so < hidden)
+      n_inter < kChunkK || n_inter % kChunkK || n_inter > kMaxInter || hidden < kTileN || hidden % kTileN ||
+      sid_t < topk || sw_t < topk || so < hidden)
     return GLM53_ERR_BAD_SHAPE;
   if (!aligned16(act) || !aligned16(w2) || (reinterpret_cast<uintptr_t>(s2) & 7) || (reinterpret_cast<uintptr_t>(out) & 1))
     return GLM53_ERR_MISALIGNED;
@@ -381,30 +472,19 @@ extern "C" int glm53_moe_w4a16_down(const void* act, const void* w2, const void*
   return static_cast<int>(hipGetLastError());
 }
 
-// Workspace of glm53_fused_moe_w4a16: aligner outputs, then the activations.
+// Workspace of glm53_fused_moe_w4a16: the c2 activations.
 namespace {
 constexpr int64_t kAlignBytes = 256;
-int64_t round_up(int64_t v) { return (v + kAlignBytes - 1) / kAlignBytes * kAlignBytes; }
-struct FusedLayout {
-  int64_t sorted, experts, postpad, act, total;
-};
-FusedLayout fused_layout(int64_t routes, int64_t n_inter) {
-  FusedLayout l;
-  l.sorted = 0;
-  l.experts = round_up(routes * kBlock * 4);
-  l.postpad = l.experts + round_up(routes * 4);
-  l.act = l.postpad + kAlignBytes;
-  l.total = l.act + round_up(routes * n_inter * 2);
-  return l;
+int64_t fused_ws_bytes(int64_t routes, int64_t n_inter) {
+  return (routes * n_inter * 2 + kAlignBytes - 1) / kAlignBytes * kAlignBytes;
 }
-constexpr int64_t kAlignerExperts = 288;
-constexpr int64_t kAlignerTopk = 8;
-constexpr int64_t kAlignerMaxTokens = 8;
+constexpr int64_t kFusedTopk = 8;
+constexpr int64_t kFusedMaxTokens = 8;
 }  // namespace
 
 extern "C" int64_t glm53_fused_moe_w4a16_workspace_bytes(int64_t num_tokens, int64_t topk, int64_t n_inter) {
   if (num_tokens < 1 || topk < 1 || n_inter < 1) return 0;
-  return fused_layout(num_tokens * topk, n_inter).total;
+  return fused_ws_bytes(num_tokens * topk, n_inter);
 }
 
 extern "C" int glm53_fused_moe_w4a16(const void* x, int64_t sx, const void* w13, const void* s13,
@@ -415,22 +495,16 @@ extern "C" int glm53_fused_moe_w4a16(const void* x, int64_t sx, const void* w13,
                                      void* stream) {
   if (!x || !w13 || !s13 || !w2 || !s2 || !topk_ids || !topk_weights || !out || !workspace)
     return GLM53_ERR_NULL_POINTER;
-  if (num_tokens < 1 || num_tokens > kAlignerMaxTokens || topk != kAlignerTopk || num_experts != kAlignerExperts)
+  if (num_tokens < 1 || num_tokens > kFusedMaxTokens || topk != kFusedTopk || num_experts != kAlignExperts)
     return GLM53_ERR_BAD_SHAPE;
   const int64_t routes = num_tokens * topk;
-  const FusedLayout l = fused_layout(routes, n_inter);
-  if (workspace_bytes < l.total) return GLM53_ERR_WORKSPACE;
+  if (workspace_bytes < fused_ws_bytes(routes, n_inter)) return GLM53_ERR_WORKSPACE;
   if (!aligned16(workspace)) return GLM53_ERR_MISALIGNED;
-  char* ws = static_cast<char*>(workspace);
-  int32_t* sorted = reinterpret_cast<int32_t*>(ws + l.sorted);
-  int32_t* experts = reinterpret_cast<int32_t*>(ws + l.experts);
-  int32_t* postpad = reinterpret_cast<int32_t*>(ws + l.postpad);
-  void* act = ws + l.act;
-  int rc = glm53_moe_align_small(topk_ids, ids_is_i64, routes, sorted, experts, postpad, stream);
+  // The gate/up kernel aligns the routes itself (the aligner's layout), so
+  // the aligner's launch and its outputs' round trip through memory go away.
+  int rc = launch_gate_up(true, x, sx, w13, s13, nullptr, nullptr, topk_ids, ids_is_i64, routes, topk, num_experts,
+                          n_inter, hidden, clamp_limit, workspace, stream);
   if (rc) return rc;
-  rc = glm53_moe_w4a16_gate_up(x, sx, w13, s13, sorted, experts, routes, topk, num_experts, n_inter, hidden,
-                               clamp_limit, act, stream);
-  if (rc) return rc;
-  return glm53_moe_w4a16_down(act, w2, s2, topk_ids, ids_is_i64, topk, topk_weights, topk, num_tokens, topk,
+  return glm53_moe_w4a16_down(workspace, w2, s2, topk_ids, ids_is_i64, topk, topk_weights, topk, num_tokens, topk,
                               num_experts, n_inter, hidden, out, so, stream);
 }

@@ -16,8 +16,7 @@ the aligner and both in one call.
 Weights arrive in the checkpoint's GPTQ / compressed-tensors packing (int32
 [E, n_out, K/8], k = 8w + i in bits 4i of word w; bf16 scales [E, n_out,
 K/32]) and are repacked once with repack_w4a16 into the kernels' tile order
-(the MI355X counterpart of Marlin's load-time repack); scales are used as
-loaded.
+(the MI355X counterpart of Marlin's load-time repack and scale permutation).
 """
 from __future__ import annotations
 
@@ -42,10 +41,10 @@ def _check_repacked(w: torch.Tensor, name: str, n_out: int, k: int) -> None:
 
 
 def _check_scale(s: torch.Tensor, name: str, e: int, n_out: int, k: int) -> None:
-    want = (e, n_out, k // GROUP)
+    want = (e, n_out // 16, k // 128, 16, 4)
     if s.dtype != torch.bfloat16 or tuple(s.shape) != want or not s.is_contiguous():
-        raise ValueError(f"{name} must be contiguous bf16 group-{GROUP} scales of shape {want}, "
-                         f"got {s.dtype} {tuple(s.shape)}")
+        raise ValueError(f"{name} must be contiguous repacked bf16 group-{GROUP} scales of shape {want} "
+                         f"(repack_w4a16 output), got {s.dtype} {tuple(s.shape)}")
 
 
 def _clamp(clamp_limit) -> float:
@@ -57,9 +56,10 @@ def _clamp(clamp_limit) -> float:
     return c
 
 
-def repack_w4a16(weight_packed: torch.Tensor) -> torch.Tensor:
-    """Checkpoint int32 [E, n_out, K/8] -> the kernels' tile order, int32
-    [E, n_out/16, K/128, 64, 4] (same bytes, reordered; n_out % 16 == 0,
+def repack_w4a16(weight_packed: torch.Tensor, weight_scale: torch.Tensor):
+    """Checkpoint int32 [E, n_out, K/8] codes and bf16 [E, n_out, K/32]
+    scales -> the kernels' tile order: (int32 [E, n_out/16, K/128, 64, 4],
+    bf16 [E, n_out/16, K/128, 16, 4]); same bytes, reordered (n_out % 16 == 0,
     K % 128 == 0).  Runs once per weight at load time."""
     if weight_packed.dtype != torch.int32 or weight_packed.dim() != 3:
         raise ValueError(f"expected int32 [E, n_out, K/8], got {weight_packed.dtype} {tuple(weight_packed.shape)}")
@@ -67,13 +67,19 @@ def repack_w4a16(weight_packed: torch.Tensor) -> torch.Tensor:
     k = 8 * kw
     if n_out % 16 or k % 128 or e == 0:
         raise ValueError(f"n_out ({n_out}) must be a multiple of 16 and K ({k}) of 128")
+    if weight_scale.dtype != torch.bfloat16 or tuple(weight_scale.shape) != (e, n_out, k // GROUP):
+        raise ValueError(f"expected bf16 scales [{e}, {n_out}, {k // GROUP}], got {weight_scale.dtype} "
+                         f"{tuple(weight_scale.shape)}")
     src = weight_packed.contiguous()
+    src_s = weight_scale.contiguous()
     out = torch.empty((e, n_out // 16, k // 128, 64, 4), dtype=torch.int32, device=src.device)
+    out_s = torch.empty((e, n_out // 16, k // 128, 16, 4), dtype=torch.bfloat16, device=src.device)
     L = _lib.load()
     with torch.cuda.device(src.device):
-        rc = L.glm53_moe_w4a16_repack(src.data_ptr(), e, n_out, k, out.data_ptr(), _lib.stream_handle(src.device))
+        rc = L.glm53_moe_w4a16_repack(src.data_ptr(), src_s.data_ptr(), e, n_out, k, out.data_ptr(),
+                                      out_s.data_ptr(), _lib.stream_handle(src.device))
     _lib.check(rc, "glm53_moe_w4a16_repack")
-    return out
+    return out, out_s
 
 
 def moe_w4a16_gate_up(hidden_states: torch.Tensor, w13: torch.Tensor, w13_scale: torch.Tensor,
@@ -146,9 +152,10 @@ def fused_moe_w4a16(hidden_states: torch.Tensor, w13: torch.Tensor, w2: torch.Te
     """The MoE layer for 1..8 decode tokens: aligner, gate/up GEMM + SiLU
     with clamp, down GEMM with router weights, sum over the 8 routes.
 
-    hidden_states bf16 [T, K]; w13 / w2 repacked (repack_w4a16) from
-    [288, 2N, K/8] / [288, K, N/8]; scales bf16 [288, 2N, K/32] /
-    [288, K, N/32]; topk_weights fp32 [T, 8]; topk_ids int32 / int64 [T, 8].
+    hidden_states bf16 [T, K]; (w13, w13_scale) and (w2, w2_scale) as
+    repack_w4a16 returns them for [288, 2N, K/8] / [288, K, N/8] codes with
+    [288, 2N, K/32] / [288, K, N/32] bf16 scales; topk_weights fp32 [T, 8];
+    topk_ids int32 / int64 [T, 8].
     Returns bf16 [T, K] (written into `output` when given).  Raises
     ValueError outside the configuration the reference's gate accepts
     (profiles/sm74/titan_prefill/marlin.py:247-295): no expert map, router

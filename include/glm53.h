@@ -237,23 +237,26 @@ int glm53_moe_align_small(const void* topk_ids, int ids_is_i64,
  * L = clamp_limit (> 0; +inf for plain SiLU-and-multiply).
  *
  * Weights: checkpoint int32 [E][n_out][K/8] (word w of row n holds k = 8w+i
- * in bits 4i, the GPTQ / compressed-tensors packing) are repacked once by
- * glm53_moe_w4a16_repack into the kernels' tile order (same size, int32
- * [E][n_out/16][K/128][64][4]); W13 is [E][2N][K] (gate rows, then up rows),
- * W2 is [E][K][N].  Scales are used as the checkpoint holds them: bf16
- * [E][n_out][K/32].  N and K are multiples of 128 (K) and 16 (N) for W13, N
- * a multiple of 128 for W2.
+ * in bits 4i, the GPTQ / compressed-tensors packing) with bf16 scales
+ * [E][n_out][K/32] are repacked once by glm53_moe_w4a16_repack into the
+ * kernels' tile order (same sizes: int32 [E][n_out/16][K/128][64][4] and
+ * bf16 [E][n_out/16][K/128][16][4]); W13 is [E][2N][K] (gate rows, then up
+ * rows), W2 is [E][K][N].  K is a multiple of 128 and N of 16 for W13, N a
+ * multiple of 128 for W2.
  */
-/* Repack [E][n_out][k/8] int32 words (w_packed, 4-byte aligned) into the
- * tile order at out (16-byte aligned, same byte size).  n_out % 16 == 0,
+/* Repack [E][n_out][k/8] int32 words (w_packed, 4-byte aligned) and their
+ * bf16 scales [E][n_out][k/32] (w_scale) into the tile order at out
+ * (16-byte aligned) and out_scale (8-byte aligned).  n_out % 16 == 0,
  * k % 128 == 0. */
-int glm53_moe_w4a16_repack(const void* w_packed, int64_t num_experts,
-                           int64_t n_out, int64_t k, void* out, void* stream);
+int glm53_moe_w4a16_repack(const void* w_packed, const void* w_scale,
+                           int64_t num_experts, int64_t n_out, int64_t k,
+                           void* out, void* out_scale, void* stream);
 
 /* c2 for every route of the aligner's blocks: one workgroup per (8-slot
  * block b with expert_ids[b] in [0, E), 16 intermediate columns); slots
  * holding num_routes are padding.  x bf16 [T][hidden], row stride sx
- * elements (16-byte aligned rows); act bf16 [num_routes][n_inter]. */
+ * elements (16-byte aligned rows), hidden <= 4096; act bf16
+ * [num_routes][n_inter]. */
 int glm53_moe_w4a16_gate_up(const void* x, int64_t sx, const void* w13,
                             const void* s13, const int32_t* sorted_ids,
                             const int32_t* expert_ids, int64_t num_routes,
@@ -262,7 +265,7 @@ int glm53_moe_w4a16_gate_up(const void* x, int64_t sx, const void* w13,
                             float clamp_limit, void* act, void* stream);
 
 /* out for every token: one workgroup per (16 output features, token), the
- * token's topk (<= 8) routes summed in slot order.  topk_ids int32 or int64
+ * token's topk (<= 8) routes summed in slot order; n_inter <= 2048.  topk_ids int32 or int64
  * (ids_is_i64) [T][topk] with row stride sid_t; topk_weights fp32 [T][topk]
  * with row stride sw_t; out bf16 [T][hidden], row stride so. */
 int glm53_moe_w4a16_down(const void* act, const void* w2, const void* s2,
@@ -272,13 +275,16 @@ int glm53_moe_w4a16_down(const void* act, const void* w2, const void* s2,
                          int64_t num_experts, int64_t n_inter,
                          int64_t hidden, void* out, int64_t so, void* stream);
 
-/* Bytes of the workspace glm53_fused_moe_w4a16 needs (aligner outputs and
- * the c2 activations). */
+/* Bytes of the workspace glm53_fused_moe_w4a16 needs (the c2 activations,
+ * bf16 [num_tokens * topk][n_inter]). */
 int64_t glm53_fused_moe_w4a16_workspace_bytes(int64_t num_tokens,
                                               int64_t topk, int64_t n_inter);
 
-/* Aligner + gate/up + down for 1..8 tokens, top-8, 288 experts (the
- * aligner's contract); topk_ids and topk_weights contiguous [T][8]. */
+/* The whole layer for 1..8 tokens, top-8, 288 experts (the aligner's
+ * contract); topk_ids and topk_weights contiguous [T][8].  Two launches: the
+ * gate/up kernel derives each workgroup's aligner block (expert and slots,
+ * the layout glm53_moe_align_small writes) from topk_ids itself, then the
+ * down kernel. */
 int glm53_fused_moe_w4a16(const void* x, int64_t sx, const void* w13,
                           const void* s13, const void* w2, const void* s2,
                           const void* topk_ids, int ids_is_i64,

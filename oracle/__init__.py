@@ -323,6 +323,14 @@ def repack_w4a16(words: np.ndarray) -> np.ndarray:
     return w.reshape(E, n // 16, K // 128, 64, 4).view(np.int32)
 
 
+def repack_w4a16_scales(scales: np.ndarray) -> np.ndarray:
+    """The scales' tile order (glm53_moe_w4a16_repack): [E, n_out, K/32] ->
+    [E, n_out/16, K/128, 16, 4]; element [e, nt, c, r, g] is the scale of row
+    16*nt + r, group 4c + g."""
+    E, n, G = scales.shape
+    return np.ascontiguousarray(scales.reshape(E, n // 16, 16, G // 4, 4).transpose(0, 1, 3, 2, 4))
+
+
 def _dequant(words: np.ndarray, scales_u16: np.ndarray) -> np.ndarray:
     """(q - 8) * s in float64 (exact), [n_out, K]."""
     q = unpack_w4(words).astype(np.float64) - 8.0

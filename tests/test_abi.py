@@ -197,11 +197,12 @@ def test_moe_w4a16_host_errors():
     fake = ctypes.c_void_p(0x10000)
     mis = ctypes.c_void_p(0x10008)
     # repack: null, shapes, alignment
-    assert L.glm53_moe_w4a16_repack(None, 288, 1024, 4096, fake, None) == -1
-    assert L.glm53_moe_w4a16_repack(fake, 288, 1000, 4096, fake, None) == -2
-    assert L.glm53_moe_w4a16_repack(fake, 288, 1024, 4000, fake, None) == -2
-    assert L.glm53_moe_w4a16_repack(fake, 0, 1024, 4096, fake, None) == -2
-    assert L.glm53_moe_w4a16_repack(fake, 288, 1024, 4096, mis, None) == -3
+    assert L.glm53_moe_w4a16_repack(None, fake, 288, 1024, 4096, fake, fake, None) == -1
+    assert L.glm53_moe_w4a16_repack(fake, None, 288, 1024, 4096, fake, fake, None) == -1
+    assert L.glm53_moe_w4a16_repack(fake, fake, 288, 1000, 4096, fake, fake, None) == -2
+    assert L.glm53_moe_w4a16_repack(fake, fake, 288, 1024, 4000, fake, fake, None) == -2
+    assert L.glm53_moe_w4a16_repack(fake, fake, 0, 1024, 4096, fake, fake, None) == -2
+    assert L.glm53_moe_w4a16_repack(fake, fake, 288, 1024, 4096, mis, fake, None) == -3
     # gate/up: x, sx, w13, s13, sorted, experts, R, topk, E, N, K, clamp, act, stream
     args = [fake, 4096, fake, fake, fake, fake, 64, 8, 288, 512, 4096, 10.0, fake, None]
     bad = lambda i, v: L.glm53_moe_w4a16_gate_up(*(args[:i] + [v] + args[i + 1:]))
@@ -223,7 +224,7 @@ def test_moe_w4a16_host_errors():
     assert bad(0, mis) == -3
     # fused: the aligner's contract (1..8 tokens, top-8, 288 experts) and the workspace
     ws = L.glm53_fused_moe_w4a16_workspace_bytes(8, 8, 512)
-    assert ws >= 64 * 512 * 2 + 64 * 8 * 4
+    assert ws >= 64 * 512 * 2                # the c2 activations of 64 routes
     args = [fake, 4096, fake, fake, fake, fake, fake, 0, fake, 8, 8, 288, 512, 4096, 10.0, fake, ws, fake,
             4096, None]
     bad = lambda i, v: L.glm53_fused_moe_w4a16(*(args[:i] + [v] + args[i + 1:]))
@@ -240,8 +241,8 @@ def test_moe_w4a16_contract_errors_on_cpu():
     x = torch.zeros(2, 4096, dtype=torch.bfloat16)
     w13 = torch.zeros(288, 64, 32, 64, 4, dtype=torch.int32)
     w2 = torch.zeros(288, 256, 4, 64, 4, dtype=torch.int32)
-    s13 = torch.zeros(288, 1024, 128, dtype=torch.bfloat16)
-    s2 = torch.zeros(288, 4096, 16, dtype=torch.bfloat16)
+    s13 = torch.zeros(288, 64, 32, 16, 4, dtype=torch.bfloat16)
+    s2 = torch.zeros(288, 256, 4, 16, 4, dtype=torch.bfloat16)
     tw = torch.zeros(2, 8)
     ids = torch.zeros(2, 8, dtype=torch.int32)
     call = lambda **kw: fused_moe_w4a16(**{**dict(hidden_states=x, w13=w13, w2=w2, w13_scale=s13,
@@ -259,10 +260,12 @@ def test_moe_w4a16_contract_errors_on_cpu():
     with pytest.raises(ValueError, match="experts"):
         call(w13=w13[:256], w2=w2[:256])
     with pytest.raises(ValueError, match="w13_scale"):
-        call(w13_scale=s13[:, :, :64])
+        call(w13_scale=torch.zeros(288, 1024, 128, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="w2"):
         call(w2=torch.zeros(288, 256, 4, 64, 2, dtype=torch.int32))
     with pytest.raises(ValueError, match="clamp_limit"):
         call(clamp_limit=0.0)
     with pytest.raises(ValueError):
-        repack_w4a16(torch.zeros(288, 1000, 512, dtype=torch.int32))
+        repack_w4a16(torch.zeros(288, 1000, 512, dtype=torch.int32), torch.zeros(288, 1000, 128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        repack_w4a16(torch.zeros(288, 1024, 512, dtype=torch.int32), torch.zeros(288, 1024, 64, dtype=torch.bfloat16))

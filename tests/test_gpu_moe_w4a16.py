@@ -32,8 +32,9 @@ def moe(cuda, oracle):
     from titan_moe_w4a16 import repack_w4a16
     log_case("moe layer: build 288 x (1024 x 4096 + 4096 x 512) W4A16 weights")
     lay = W.moe_w4a16_layer(cuda, seed=W.SEED_FIXTURE)
-    dev = {"w13": repack_w4a16(lay["w13_packed"]), "w2": repack_w4a16(lay["w2_packed"]),
-           "w13_scale": lay["w13_scale"], "w2_scale": lay["w2_scale"]}
+    w13, s13 = repack_w4a16(lay["w13_packed"], lay["w13_scale"])
+    w2, s2 = repack_w4a16(lay["w2_packed"], lay["w2_scale"])
+    dev = {"w13": w13, "w2": w2, "w13_scale": s13, "w2_scale": s2}
     host = {k: v.cpu().numpy() if v.dtype != torch.bfloat16 else v.view(torch.int16).cpu().numpy().view(np.uint16)
             for k, v in lay.items()}
     torch.cuda.synchronize()
@@ -71,12 +72,18 @@ def test_repack_bit_exact(cuda, oracle, moe):
     from titan_moe_w4a16 import repack_w4a16
     g = torch.Generator(device=cuda).manual_seed(5)
     small = torch.randint(0, 256, (3, 48, 192), generator=g, device=cuda, dtype=torch.uint8).view(torch.int32)
+    small_s = torch.randint(0, 2**15, (3, 48, 12), generator=g, device=cuda, dtype=torch.int16).view(torch.bfloat16)
     log_case("repack [3, 48, 48] words")
-    got = repack_w4a16(small).cpu().numpy()
-    assert np.array_equal(got, oracle.repack_w4a16(small.cpu().numpy()))
+    got, got_s = repack_w4a16(small, small_s)
+    assert np.array_equal(got.cpu().numpy(), oracle.repack_w4a16(small.cpu().numpy()))
+    assert np.array_equal(got_s.view(torch.int16).cpu().numpy(),
+                          oracle.repack_w4a16_scales(small_s.view(torch.int16).cpu().numpy()))
     for name in ("w13", "w2"):
         want = oracle.repack_w4a16(moe["host"][name + "_packed"][[0, 141, 287]])
         assert np.array_equal(moe["dev"][name][[0, 141, 287]].cpu().numpy(), want), name
+        want_s = oracle.repack_w4a16_scales(moe["host"][name + "_scale"][[0, 141, 287]])
+        got_s = moe["dev"][name + "_scale"][[0, 141, 287]].view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(got_s, want_s), name + "_scale"
 
 
 @pytest.mark.parametrize("batch", [1, 2, 4, 8])

@@ -60,6 +60,15 @@ def test_repack_layout_brute_force(oracle):
                             assert (word >> bit) & 0xF == codes[e, 16 * nt + lane % 16, k]
 
 
+def test_scale_repack_layout_brute_force(oracle):
+    rng = np.random.default_rng(7)
+    sc = rng.integers(0, 2**16, size=(2, 48, 12), dtype=np.uint16)
+    t = oracle.repack_w4a16_scales(sc)
+    assert t.shape == (2, 3, 3, 16, 4)
+    for e, nt, c, r, g in np.ndindex(*t.shape):
+        assert t[e, nt, c, r, g] == sc[e, 16 * nt + r, 4 * c + g]
+
+
 def test_magic_decode_is_code_plus_128():
     # (word >> 4j) & 0x000F000F | 0x43004300 read as two bf16 = 128 + code
     for code in range(16):
