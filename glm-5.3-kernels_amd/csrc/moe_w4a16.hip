@@ -125,6 +125,7 @@ struct GateUpArgs {
   int num_routes;           // R = T * topk (padding value of sorted_ids)
   int topk;
   int topk_log2;            // log2(topk) when topk is a power of two, else -1
+  int tiles_per_wg;         // 16-column tiles per workgroup
   int num_experts;
   int n_inter;              // N
   int hidden;               // K
@@ -132,9 +133,9 @@ struct GateUpArgs {
   uint16_t* act;            // bf16 [R][N]
 };
 
-union __align__(16) GateUpShared {
+struct __align__(16) GateUpShared {
   uint16_t x[kBlock][kXStride];            // the block's activation rows
-  float red[kWaves][2][4][64];             // partial tiles, after the last x read
+  f32x4 red[2][kWaves][2][64];             // partial tiles [buffer][wave][gate/up][lane]
 };
 
 // The MFMA loop over this wave's chunks of a gate tile and an up tile.
@@ -171,14 +172,131 @@ __device__ __forceinline__ void gate_up_chunks(const uint16_t* xs, int c_lo, int
   }
 }
 
+// Workgroup barrier for LDS traffic only: this wave's LDS accesses are
+// complete (lgkmcnt 0) and no memory access moves across it.  Unlike
+// __syncthreads(), whose release fence waits for every outstanding global
+// load (vmcnt 0), it keeps the next tile's weight loads in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One gate/up tile pair's operands for this wave: codes and scales of its
+// chunks of the gate tile and of the up tile.
+struct TileRegs {
+  uint4 kg[kBatch], ku[kBatch];
+  uint2 scg[kBatch], scu[kBatch];
+};
+
+__device__ __forceinline__ void load_tile(TileRegs& t, const GateUpArgs& a, int e, int jt, int c_lo, int cpw,
+                                          int k_chunks, int lane, int col) {
+  // Uniform tile bases (SGPRs) plus 32-bit lane offsets: each load is
+  // base + lane offset + an immediate chunk offset.
+  const int n_tiles13 = 2 * a.n_inter / kTileN;
+  const int64_t tg = (static_cast<int64_t>(e) * n_tiles13 + jt) * k_chunks + c_lo;
+  const int64_t tu = tg + static_cast<int64_t>(a.n_inter / kTileN) * k_chunks;
+  const uint4* wg = a.w13 + tg * 64;
+  const uint4* wu = a.w13 + tu * 64;
+  const uint16_t* sg = a.s13 + tg * 64;
+  const uint16_t* su = a.s13 + tu * 64;
+#pragma unroll
+  for (int u = 0; u < kBatch; u++) {   // chunks past the wave's range re-read its last one (not used)
+    const int uu = c_lo + (u < cpw ? u : cpw - 1) < k_chunks ? (u < cpw ? u : cpw - 1) : k_chunks - 1 - c_lo;
+    t.kg[u] = wg[64 * uu + lane];
+    t.ku[u] = wu[64 * uu + lane];
+    t.scg[u] = *reinterpret_cast<const uint2*>(sg + 64 * uu + 4 * col);
+    t.scu[u] = *reinterpret_cast<const uint2*>(su + 64 * uu + 4 * col);
+  }
+  // Keep the loads here: the scheduler would otherwise sink them toward
+  // their uses (behind the previous tile's compute), defeating the prefetch.
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Sum the 8 waves' partial tiles (fixed order), SiLU-and-multiply, store c2.
+__device__ __forceinline__ void finish_tile(GateUpShared& sh, int buf, const GateUpArgs& a, int jt,
+                                            const int (&slot)[kBlock], const f32x4& acc_g, const f32x4& acc_u,
+                                            int w, int lane) {
+  sh.red[buf][w][0][lane] = acc_g;
+  sh.red[buf][w][1][lane] = acc_u;
+  lds_barrier();
+  if (threadIdx.x < kTileN * kBlock) {
+    const int n = threadIdx.x & 15;
+    const int m = threadIdx.x >> 4;   // slot 0..7: D row m sits in lane n + 16*(m/4), element m%4
+    int route = a.num_routes;
+#pragma unroll
+    for (int mm = 0; mm < kBlock; mm++)
+      if (m == mm) route = slot[mm];
+    if (route < a.num_routes) {
+      const float* rg = reinterpret_cast<const float*>(&sh.red[buf][0][0][n + 16 * (m >> 2)]) + (m & 3);
+      const float* ru = reinterpret_cast<const float*>(&sh.red[buf][0][1][n + 16 * (m >> 2)]) + (m & 3);
+      float g = 0.f, up = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ww++) {   // wave stride: 2 * 64 float4
+        g += rg[ww * 2 * 64 * 4];
+        up += ru[ww * 2 * 64 * 4];
+      }
+      g = fminf(bf16_round(g), a.clamp);
+      up = fminf(fmaxf(bf16_round(up), -a.clamp), a.clamp);
+      const float v = g / (1.0f + expf(-g)) * up;
+      a.act[static_cast<int64_t>(route) * a.n_inter + kTileN * jt + n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    }
+  }
+}
+
+template <bool kSingle>
+__device__ __forceinline__ void tile_step(GateUpShared& sh, int& buf, const GateUpArgs& a, int jt,
+                                          const int (&slot)[kBlock], const uint16_t* xs, int c_lo, int cpw,
+                                          int k_chunks, const TileRegs& t, int w, int lane) {
+  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
+  gate_up_chunks<kSingle>(xs, c_lo, cpw, k_chunks, t.kg, t.ku, t.scg, t.scu, acc_g, acc_u);
+  finish_tile(sh, buf, a, jt, slot, acc_g, acc_u, w, lane);
+  buf ^= 1;
+}
+
+// The tiles [jt0, jt_end) of one block (jt_end - jt0 <= kTpw), fully
+// unrolled: the next tile's loads are in flight while a tile is computed and
+// finished (two register sets, two reduction buffers, one workgroup barrier
+// per tile).  Loads past jt_end re-read the last tile, so every register set
+// is defined on every path and no load waits on a branch merge.
+template <bool kSingle, int kTpw>
+__device__ __forceinline__ void gate_up_tiles(GateUpShared& sh, const GateUpArgs& a, int e, int jt0, int jt_end,
+                                              const int (&slot)[kBlock], const uint16_t* xs, int c_lo, int cpw,
+                                              int k_chunks, TileRegs (&t)[2], int w, int lane, int col) {
+  int buf = 0;
+#pragma unroll
+  for (int i = 0; i < kTpw; i++) {
+    if (i + 1 < kTpw) {
+      const int jn = jt0 + i + 1 < jt_end ? jt0 + i + 1 : jt_end - 1;
+      load_tile(t[(i + 1) & 1], a, e, jn, c_lo, cpw, k_chunks, lane, col);
+    }
+    if (jt0 + i < jt_end)   // uniform
+      tile_step<kSingle>(sh, buf, a, jt0 + i, slot, xs, c_lo, cpw, k_chunks, t[i & 1], w, lane);
+  }
+}
+
+template <bool kSingle>
+__device__ __forceinline__ void gate_up_dispatch(GateUpShared& sh, const GateUpArgs& a, int e, int jt0, int jt_end,
+                                                 const int (&slot)[kBlock], const uint16_t* xs, int c_lo, int cpw,
+                                                 int k_chunks, TileRegs (&t)[2], int w, int lane, int col) {
+  switch (a.tiles_per_wg) {
+    case 1: gate_up_tiles<kSingle, 1>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col); break;
+    case 2: gate_up_tiles<kSingle, 2>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col); break;
+    case 4: gate_up_tiles<kSingle, 4>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col); break;
+    default: gate_up_tiles<kSingle, 8>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col); break;
+  }
+}
+
 // kSelfAlign: the workgroup derives its aligner block (expert and 8 slots)
 // from the routes itself, with the aligner's ballots, instead of loading
 // sorted_ids / expert_ids: one launch and one dependent load fewer.
+// Workgroup (b, g) computes tiles [g * tiles_per_wg, +tiles_per_wg) of block b.
 template <bool kSelfAlign>
 __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateUpArgs a) {
   __shared__ GateUpShared sh;
   const int b = blockIdx.x;
-  const int jt = blockIdx.y;
+  const int n_half = a.n_inter / kTileN;
+  const int jt0 = blockIdx.y * a.tiles_per_wg;
+  const int jt_end = jt0 + a.tiles_per_wg < n_half ? jt0 + a.tiles_per_wg : n_half;
+  if (jt0 >= n_half) return;
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   const int q = lane >> 4, col = lane & 15;
@@ -202,41 +320,32 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
   }
   if (e < 0 || e >= a.num_experts) return;   // unused block (uniform over the workgroup)
 
-  // Wave w owns chunks [cpw*w, cpw*w + cpw) of K (cpw <= kBatch).  It stages
-  // the block's activation rows over that range into LDS with direct
-  // global->LDS loads (lane i -> 16 bytes at i*16; no VGPRs), so the MFMA
-  // loop reads only what this wave loaded and needs no workgroup barrier.
+  // Wave w owns chunks [cpw*w, cpw*w + cpw) of K (cpw <= kBatch) and stages
+  // the block's activation rows over that range into LDS once; the MFMA loop
+  // reads only what this wave wrote, so no barrier is needed before it.
+  // Slot 0 (always routed) is loaded before the first tile's weights and
+  // stored after them, so its latency hides under theirs; further routed
+  // slots (blocks shared by several tokens) follow one by one.  (Plain loads,
+  // not global->LDS DMA: pending DMA makes the compiler wait for every
+  // outstanding load before each LDS access, which would drain the weight
+  // prefetch at every tile.)
   const int k_chunks = a.hidden / kChunkK;
   const int cpw = (k_chunks + kWaves - 1) / kWaves;
   const int c_lo = cpw * w;
   const int kbase = kChunkK * c_lo;                 // first feature of this wave
-  const bool x_lane = 8 * lane < kChunkK * cpw && kbase + 8 * lane < a.hidden;
+  const int xo = kbase + 8 * (8 * lane < kChunkK * cpw && kbase + 8 * lane < a.hidden ? lane : 0);
+  auto x_row = [&](int route) {
+    const unsigned r = static_cast<unsigned>(route);
+    const unsigned tok = a.topk_log2 >= 0 ? r >> a.topk_log2 : r / static_cast<unsigned>(a.topk);
+    return reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(tok) * a.sx + xo);
+  };
+  const uint4 x0 = *x_row(slot[0]);
+  TileRegs t[2];
+  load_tile(t[0], a, e, jt0, c_lo, cpw, k_chunks, lane, col);
+  *reinterpret_cast<uint4*>(&sh.x[0][xo]) = x0;
 #pragma unroll
-  for (int m = 0; m < kBlock; m++) {
-    if (slot[m] < R && x_lane) {
-      const unsigned route = static_cast<unsigned>(slot[m]);
-      const unsigned tok = a.topk_log2 >= 0 ? route >> a.topk_log2 : route / static_cast<unsigned>(a.topk);
-      __builtin_amdgcn_global_load_lds(a.x + static_cast<int64_t>(tok) * a.sx + kbase + 8 * lane,
-                                       &sh.x[m][kbase], 16, 0, 0);
-    }
-  }
-
-  // This wave's chunks of the gate and up tiles and their scales.
-  const int n_tiles13 = 2 * a.n_inter / kTileN;
-  const uint4* wg = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + jt) * k_chunks) * 64 + lane;
-  const uint4* wu = a.w13 + ((static_cast<int64_t>(e) * n_tiles13 + a.n_inter / kTileN + jt) * k_chunks) * 64 + lane;
-  const uint16_t* sg = a.s13 + ((static_cast<int64_t>(e) * n_tiles13 + jt) * k_chunks) * 64 + 4 * col;
-  const uint16_t* su = a.s13 + ((static_cast<int64_t>(e) * n_tiles13 + a.n_inter / kTileN + jt) * k_chunks) * 64 + 4 * col;
-  uint4 kg[kBatch], ku[kBatch];
-  uint2 scg[kBatch], scu[kBatch];
-#pragma unroll
-  for (int u = 0; u < kBatch; u++) {   // chunks past the wave's range re-read its last one (not used)
-    const int c = c_lo + (u < cpw ? u : cpw - 1) < k_chunks ? c_lo + (u < cpw ? u : cpw - 1) : k_chunks - 1;
-    kg[u] = wg[static_cast<int64_t>(c) * 64];
-    ku[u] = wu[static_cast<int64_t>(c) * 64];
-    scg[u] = *reinterpret_cast<const uint2*>(sg + 64 * c);
-    scu[u] = *reinterpret_cast<const uint2*>(su + 64 * c);
-  }
+  for (int m = 1; m < kBlock; m++)
+    if (slot[m] < R) *reinterpret_cast<uint4*>(&sh.x[m][xo]) = *x_row(slot[m]);
 
   // A-operand row of this lane (m = col): padding slots and m >= 8 read row 0
   // (their D rows are discarded), so a block with one route reads one row.
@@ -246,43 +355,13 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
     if ((col & 7) == m && slot[m] < R) xrow = m;
   const uint16_t* xs = &sh.x[xrow][8 * q];
 
-  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
-  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's staged rows are in LDS
   bool single = true;                   // only slot 0 routed: D row 0 is the only one kept
 #pragma unroll
   for (int m = 1; m < kBlock; m++) single = single && slot[m] >= R;
   if (single)
-    gate_up_chunks<true>(xs, c_lo, cpw, k_chunks, kg, ku, scg, scu, acc_g, acc_u);
+    gate_up_dispatch<true>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col);
   else
-    gate_up_chunks<false>(xs, c_lo, cpw, k_chunks, kg, ku, scg, scu, acc_g, acc_u);
-
-  __syncthreads();   // every wave is done with x: red reuses its space
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    sh.red[w][0][r][lane] = acc_g[r];
-    sh.red[w][1][r][lane] = acc_u[r];
-  }
-  __syncthreads();
-  if (threadIdx.x < kTileN * kBlock) {
-    const int n = threadIdx.x & 15;
-    const int m = threadIdx.x >> 4;   // slot 0..7: D row m sits in lane n + 16*(m/4), element m%4
-    int route = R;
-#pragma unroll
-    for (int mm = 0; mm < kBlock; mm++)
-      if (m == mm) route = slot[mm];
-    if (route < R) {
-      float g = 0.f, up = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < kWaves; ww++) {
-        g += sh.red[ww][0][m & 3][n + 16 * (m >> 2)];
-        up += sh.red[ww][1][m & 3][n + 16 * (m >> 2)];
-      }
-      g = fminf(bf16_round(g), a.clamp);
-      up = fminf(fmaxf(bf16_round(up), -a.clamp), a.clamp);
-      const float v = g / (1.0f + expf(-g)) * up;
-      a.act[static_cast<int64_t>(route) * a.n_inter + kTileN * jt + n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
-    }
-  }
+    gate_up_dispatch<false>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col);
 }
 
 // ------------------------------------------------------------------ down
@@ -413,6 +492,19 @@ extern "C" int glm53_moe_w4a16_repack(const void* w_packed, const void* w_scale,
 
 namespace {
 
+// Compute units of the current device (cached per device).
+int num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int launch_gate_up(bool self_align, const void* x, int64_t sx, const void* w13, const void* s13,
                    const int32_t* sorted_ids, const int32_t* expert_ids, const void* topk_ids, int ids_is_i64,
                    int64_t num_routes, int64_t topk, int64_t num_experts, int64_t n_inter, int64_t hidden,
@@ -426,12 +518,19 @@ int launch_gate_up(bool self_align, const void* x, int64_t sx, const void* w13, 
   if (!aligned16(x) || sx % 8 || !aligned16(w13) || (reinterpret_cast<uintptr_t>(s13) & 7) ||
       (reinterpret_cast<uintptr_t>(act) & 1))
     return GLM53_ERR_MISALIGNED;
+  // Enough tiles per workgroup that the blocks' workgroups about fill the
+  // CUs once (each block has n_inter / 16 tiles; at most num_routes blocks).
+  const int64_t n_half = n_inter / kTileN;
+  const int64_t want = (n_half * num_routes + num_cus() - 1) / num_cus();
+  int64_t tpw = 1;                       // a power of two up to 8 (the kernel's unrolled variants)
+  while (tpw < want && tpw < 8) tpw *= 2;
   GateUpArgs a{static_cast<const uint16_t*>(x), sx, static_cast<const uint4*>(w13),
                static_cast<const uint16_t*>(s13), sorted_ids, expert_ids, topk_ids, ids_is_i64,
                static_cast<int>(num_routes), static_cast<int>(topk),
-               (topk & (topk - 1)) ? -1 : __builtin_ctzll(static_cast<uint64_t>(topk)), static_cast<int>(num_experts),
-               static_cast<int>(n_inter), static_cast<int>(hidden), clamp_limit, static_cast<uint16_t*>(act)};
-  const dim3 grid(static_cast<unsigned>(num_routes), static_cast<unsigned>(n_inter / kTileN));
+               (topk & (topk - 1)) ? -1 : __builtin_ctzll(static_cast<uint64_t>(topk)), static_cast<int>(tpw),
+               static_cast<int>(num_experts), static_cast<int>(n_inter), static_cast<int>(hidden), clamp_limit,
+               static_cast<uint16_t*>(act)};
+  const dim3 grid(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + tpw - 1) / tpw));
   (void)hipGetLastError();
   if (self_align)
     hipLaunchKernelGGL(moe_w4a16_gate_up_kernel<true>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
