@@ -310,6 +310,47 @@ def main():
         extra["moe_align_us_per_call"] = moe
         extra["moe_align_reference_us_per_call_sm80"] = {"B1": 1.63, "B2": 1.97, "B4": 1.97, "B8": 5.07}
 
+        # ------------------------------------------------------------ MoE W4A16 layer
+        # The aligner's consumer: gate/up GEMM + SiLU, down GEMM + router
+        # weights + route sum (288 experts, hidden 4096, intermediate 512).
+        # "same call": one call replayed, so a small batch's experts stay in
+        # the 256 MB MALL.  "layer rotation" (the decode case): 8 calls per
+        # graph cycling over 4 layers' weights (4 x 1.06 GB) with fresh random
+        # routes per call, as consecutive MoE layers read other experts.
+        from titan_moe_w4a16 import fused_moe_w4a16, repack_w4a16
+        layers = []
+        for li in range(4):
+            lay = W.moe_w4a16_layer(dev, seed=W.SEED_BENCH + 100 + li)
+            layers.append(repack_w4a16(lay["w13_packed"], lay["w13_scale"]) +
+                          repack_w4a16(lay["w2_packed"], lay["w2_scale"]))
+            del lay
+        moew = {}
+        for b in (1, 2, 4, 8):
+            gmw = W.gen(dev, W.SEED_BENCH + b)
+            calls = []
+            for i in range(8):
+                xm, idm, twm = W.moe_w4a16_inputs(b, dev, gmw)
+                calls.append((xm, idm, twm, layers[i % 4]))
+            one = lambda c=calls[0]: fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1])
+            rot = lambda: [fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1]) for c in calls]
+            gw, _ = capture(torch, one, args.unroll)
+            gr, _ = capture(torch, rot, 1)
+            for _ in range(3):
+                gw.replay()
+                gr.replay()
+            log(f"moe w4a16 B={b}")
+            us_same = timer.replay_loop(gw, max(2, K // args.unroll // 2)) / args.unroll
+            us_rot = timer.replay_loop(gr, max(4, K // 8)) / len(calls)
+            mb = statistics.mean(W.moe_w4a16_bytes(c[1], b) for c in calls)
+            moew[f"B{b}"] = {"us_per_call_same_call": round(us_same, 2),
+                             "us_per_call_layer_rotation": round(us_rot, 2),
+                             "algorithmic_bytes_mean": round(mb),
+                             "gbs_layer_rotation": round(mb / (us_rot * 1e-6) / 1e9, 1),
+                             "hbm_frac_layer_rotation": round(mb / (us_rot * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
+            del gw, gr, calls
+        extra["moe_w4a16_layer"] = moew
+        del layers
+
         # ------------------------------------------------------------ prefill-shaped
         qp, idxp, new_rows, pslots = W.prefill_inputs(dev, g8)
         pg, _ = capture(torch, lambda: triton_mla_sparse_attention(qp, kv8, idxp, W.SM_SCALE))
