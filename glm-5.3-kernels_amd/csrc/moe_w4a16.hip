@@ -3,8 +3,8 @@
 // experts, hidden 4096, per-rank expert intermediate 512).
 //
 // The computation is the one vLLM's fused Marlin MoE performs at that call
-// site (profiles/sm74/titan_prefill/marlin.py:384-437 composes it from the
-// same pieces; its gate, marlin.py:247-295, fixes the geometry):
+// site (profiles/sm74/titan_prefill/marlin.py:424-444 composes it from the
+// same pieces; its gate, marlin.py:255-310, fixes the geometry):
 //   c1[r]  = bf16(x[token(r)] . W13[e(r)]^T)               [R, 2N]
 //   c2[r]  = bf16(silu(min(gate, L)) * clamp(up, -L, L))   [R, N], gate = c1[r, :N], up = c1[r, N:]
 //   c3[r]  = bf16(w_r * (c2[r] . W2[e(r)]^T))               [R, K]

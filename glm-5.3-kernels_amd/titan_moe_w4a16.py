@@ -5,8 +5,8 @@ aligner (titan_moe_align.titan_moe_align_small) in a GLM-5.3 decode MoE layer.
 At the reference's call site (integration/patch_moe_align.py:17-44) the
 aligner's sorted_ids / expert_ids / postpad feed vLLM's fused Marlin MoE:
 two moe_wna16_marlin_gemm launches around a SiLU-and-multiply with clamp,
-then moe_sum (the sequence profiles/sm74/titan_prefill/marlin.py:384-437 runs;
-its gate, marlin.py:247-295, fixes the geometry: bf16 activations, E = 288,
+then moe_sum (the sequence profiles/sm74/titan_prefill/marlin.py:424-444 runs;
+its gate, marlin.py:255-310, fixes the geometry: bf16 activations, E = 288,
 top-8, hidden 4096, per-rank intermediate 512 under TP4, uint4b8 codes with
 bf16 group-32 scales, no zero points, clamp limit 10, router weight applied
 to the output).  This module computes the same layer with two gfx950 kernels
@@ -158,7 +158,7 @@ def fused_moe_w4a16(hidden_states: torch.Tensor, w13: torch.Tensor, w2: torch.Te
     topk_ids int32 / int64 [T, 8].
     Returns bf16 [T, K] (written into `output` when given).  Raises
     ValueError outside the configuration the reference's gate accepts
-    (profiles/sm74/titan_prefill/marlin.py:247-295): no expert map, router
+    (profiles/sm74/titan_prefill/marlin.py:255-310): no expert map, router
     weight on the output, 288 experts, top-8, 1..8 tokens."""
     if expert_map is not None:
         raise ValueError("expert_map (expert parallelism) is not supported")

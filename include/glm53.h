@@ -221,8 +221,8 @@ int glm53_moe_align_small(const void* topk_ids, int ids_is_i64,
  * W4A16 group-32 MoE expert GEMMs: the consumer of glm53_moe_align_small.
  * Replace the two moe_wna16_marlin_gemm launches, the activation and the
  * moe_sum of vLLM's fused Marlin MoE at the GLM-5.3 call site (the call
- * sequence profiles/sm74/titan_prefill/marlin.py:384-437, gated on
- * marlin.py:247-295: bf16 activations, uint4b8 weights with bf16 group-32
+ * sequence profiles/sm74/titan_prefill/marlin.py:424-444, gated on
+ * marlin.py:255-310: bf16 activations, uint4b8 weights with bf16 group-32
  * scales and no zero points, SiLU with clamp, router weight on the output;
  * the aligner's call site integration/patch_moe_align.py:17-44).
  *

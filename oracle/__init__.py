@@ -36,7 +36,7 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
   q = 0 gives the mean row).
 * moe_w4a16 (+ unpack_w4 / pack_w4 / repack_w4a16), the expert GEMMs after
   the aligner (vLLM's fused Marlin MoE at integration/patch_moe_align.py:
-  17-44, composed as profiles/sm74/titan_prefill/marlin.py:384-437): bit
+  17-44, composed as profiles/sm74/titan_prefill/marlin.py:424-444): bit
   brute force of the packing and of the tile order, closed forms from
   uniform weights and from single codes per expert (every index of the
   layer), the SiLU clamp, route invariants and an independent torch
@@ -292,7 +292,7 @@ def expand_pools(pool_ids: np.ndarray, seq_lens, pool_size: int, out_cols: int |
 # --------------------------------------------------------------------------
 # W4A16 group-32 MoE expert GEMMs (the consumer of moe_align; vLLM's fused
 # Marlin MoE at integration/patch_moe_align.py:17-44, composed as in
-# profiles/sm74/titan_prefill/marlin.py:384-437)
+# profiles/sm74/titan_prefill/marlin.py:424-444)
 # --------------------------------------------------------------------------
 
 def unpack_w4(words: np.ndarray) -> np.ndarray:
