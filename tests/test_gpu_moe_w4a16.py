@@ -200,3 +200,29 @@ def test_graph_replay_deterministic(cuda, moe):
         assert torch.equal(captured, eager), f"replay {i}"
         fn()                                          # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_whole_experts_n2048(cuda, oracle):
+    """The gate's other width (profiles/sm74/titan_prefill/marlin.py:94:
+    N = 2048, whole experts under pipeline parallelism): 288 x 4096 x 2048
+    weights, two tokens, against the oracle on the experts the routes use."""
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16, repack_w4a16
+    log_case("moe layer N=2048: build 288 x (4096 x 4096 + 4096 x 2048) W4A16 weights")
+    lay = W.moe_w4a16_layer(cuda, seed=W.SEED_FIXTURE + 7, inter=2048)
+    w13, s13 = repack_w4a16(lay["w13_packed"], lay["w13_scale"])
+    w2, s2 = repack_w4a16(lay["w2_packed"], lay["w2_scale"])
+    g = torch.Generator(device=cuda).manual_seed(2048)
+    x, ids, tw = W.moe_w4a16_inputs(2, cuda, g)
+    ids[1, :2] = ids[0, :2]                       # two experts shared by both tokens
+    log_case("fused moe N=2048 B=2")
+    out = fused_moe_w4a16(x, w13, w2, s13, s2, tw, ids)
+    torch.cuda.synchronize()
+    used = torch.unique(ids.flatten().long())
+    local = torch.searchsorted(used, ids.long()).to(torch.int32)
+    pick = lambda t: t.index_select(0, used).contiguous()
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    want, _ = oracle.moe_w4a16(bits(x), pick(lay["w13_packed"]).cpu().numpy(), bits(pick(lay["w13_scale"])),
+                               pick(lay["w2_packed"]).cpu().numpy(), bits(pick(lay["w2_scale"])),
+                               tw.cpu().numpy(), local.cpu().numpy())
+    assert_out_close(out, want, oracle, "N=2048 B=2")
