@@ -31,6 +31,8 @@ EXPORTED = (
     "glm53_moe_w4a16_down",
     "glm53_fused_moe_w4a16_workspace_bytes",
     "glm53_fused_moe_w4a16",
+    "glm53_fp8_paged_mqa_logits",
+    "glm53_indexer_topk",
 )
 
 _lib = None
@@ -89,6 +91,11 @@ def load():
     L.glm53_fused_moe_w4a16.restype = I
     L.glm53_fused_moe_w4a16.argtypes = [P, I64, P, P, P, P, P, I, P, I64, I64, I64, I64, I64, F, P, I64,
                                         P, I64, P]
+    L.glm53_fp8_paged_mqa_logits.restype = I
+    L.glm53_fp8_paged_mqa_logits.argtypes = [P, I64, I64, P, I64, I64, I64, P, I64, P, P, I64, I64, I64, I64,
+                                             I64, I64, I, P, I64, P]
+    L.glm53_indexer_topk.restype = I
+    L.glm53_indexer_topk.argtypes = [P, I64, P, I64, I64, I64, P, I64, P]
     version = L.glm53_abi_version()
     if version != ABI_VERSION:
         raise ImportError(f"{LIB_PATH} has ABI version {version}, expected {ABI_VERSION}")

@@ -294,6 +294,45 @@ int glm53_fused_moe_w4a16(const void* x, int64_t sx, const void* w13,
                           int64_t workspace_bytes, void* out, int64_t so,
                           void* stream);
 
+/*
+ * Sparse indexer decode scoring: FP8 paged MQA logits.
+ * Replaces vLLM's fp8_paged_mqa_logits_triton as the reference's decode
+ * indexer calls it (integration/patch_decode_indexer.py:34-44, pool-granular
+ * context); semantics of DeepGEMM's fp8_paged_mqa_logits:
+ *   logits[t, j] = sum_h weights[t, h] * max(0, s_j * (q[t, h, :] . k_j))
+ * for j < context_lens[t]; -inf where block_table[t, j / block_size] is not
+ * in [0, num_blocks); positions in [context_lens[t], max_len) are set to -inf
+ * when clean_logits, else left untouched.
+ *   q        fp8 E4M3 (OCP) [T][H][128], byte strides sq_t, sq_h (16-byte aligned)
+ *   kv_cache pages of page_bytes bytes: block_size keys x 128 fp8 bytes, then
+ *            block_size fp32 scales (the fused layout [num_blocks, block_size,
+ *            1, 132]); key j of row t lives in page block_table[t, j / block_size]
+ *   weights  fp32 [T][H] (row stride sw_t); H in {16, 32, 48, 64}
+ *   logits   fp32 [T][max_len] (row stride sl_t)
+ */
+int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t sq_h,
+                               const void* kv_cache, int64_t page_bytes,
+                               int64_t block_size, int64_t num_blocks,
+                               const float* weights, int64_t sw_t,
+                               const int32_t* context_lens,
+                               const int32_t* block_table, int64_t bt_stride,
+                               int64_t max_blocks, int64_t num_tokens,
+                               int64_t num_heads, int64_t head_dim,
+                               int64_t max_len, int clean_logits,
+                               float* logits, int64_t sl_t, void* stream);
+
+/*
+ * Top-k per row of the indexer logits: the top-512 pool selection whose pool
+ * ids (topk_dst / pool_topk) the kpool expansion consumes
+ * (integration/patch_indexer_sharding.py:58-79,
+ * integration/patch_decode_indexer.py:64-72; vLLM's radix top-k): the k largest of logits[r, 0 : lengths[r]] (NaN ranks
+ * lowest, ties by smaller position), written as positions in ascending order;
+ * a row with fewer than k valid positions gets all of them, then -1.
+ */
+int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t* lengths,
+                       int64_t num_rows, int64_t max_len, int64_t k,
+                       int32_t* out, int64_t so, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

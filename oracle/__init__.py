@@ -386,3 +386,85 @@ def moe_w4a16(x_u16: np.ndarray, w13: np.ndarray, s13: np.ndarray, w2: np.ndarra
     for j in range(topk):
         out += c3[:, j]
     return f32_to_bf16(out), act
+
+
+# --------------------------------------------------------------------------
+# Sparse indexer decode scoring: FP8 paged MQA logits (DeepGEMM's published
+# fp8_paged_mqa_logits semantics; vLLM's fp8_paged_mqa_logits_triton as the
+# reference calls it, integration/patch_decode_indexer.py:34-44) and the
+# top-k pool selection (integration/patch_decode_indexer.py:64-72)
+# --------------------------------------------------------------------------
+
+def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
+    """OCP FP8 E4M3 (e4m3fn) bytes -> float32: bias 7, subnormals m * 2^-9,
+    0x7F / 0xFF NaN, no infinities."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    out = sign * mag
+    out = np.where((c & 0x7F) == 0x7F, np.nan, out)
+    return out.astype(np.float32)
+
+
+def fp8_paged_mqa_logits(q_u8: np.ndarray, pages: np.ndarray, block_size: int, weights: np.ndarray,
+                         context_lens: np.ndarray, block_table: np.ndarray, max_len: int,
+                         clean: bool = True, bound: bool = False):
+    """q_u8 uint8 [T, H, 128]; pages uint8 [num_blocks, page_bytes] (block_size
+    x 128 key bytes, then block_size float32 scales); weights [T, H]; per-row
+    context_lens [T] and block_table [T, max_blocks].  Returns float64 logits
+    [T, max_len] (NaN where not written: positions >= context when not clean);
+    with bound=True also the float64 sum over heads and dims of
+    |w s q k| (the magnitude an fp32 accumulation error scales with)."""
+    T, H, D = q_u8.shape
+    nb = pages.shape[0]
+    table = e4m3_to_f32(np.arange(256, dtype=np.uint8)).astype(np.float64)
+    out = np.full((T, max_len), np.nan)
+    mag = np.zeros((T, max_len))
+    cap = block_table.shape[1] * block_size
+    for t in range(T):
+        n = int(min(max(int(context_lens[t]), 0), cap))
+        if clean:
+            out[t, n:] = -np.inf
+        n = min(n, max_len)
+        j = np.arange(n)
+        blk = np.asarray(block_table[t, j // block_size], dtype=np.int64)
+        ok = (blk >= 0) & (blk < nb)
+        off = j % block_size
+        b = np.where(ok, blk, 0)
+        kbytes = pages[b[:, None], off[:, None] * D + np.arange(D)[None, :]]          # [n, D]
+        sbytes = pages[b[:, None], block_size * D + 4 * off[:, None] + np.arange(4)[None, :]]
+        s = np.ascontiguousarray(sbytes).view(np.float32).reshape(n).astype(np.float64)
+        k = table[kbytes]
+        q = table[q_u8[t]]                                                             # [H, D]
+        w = np.asarray(weights[t], dtype=np.float64)
+        dots = k @ q.T                                                                 # [n, H]
+        val = (np.maximum(s[:, None] * dots, 0.0) * w[None, :]).sum(axis=1)
+        out[t, :n] = np.where(ok, val, -np.inf)
+        if bound:
+            mag[t, :n] = np.where(ok, (np.abs(s)[:, None] * (np.abs(k) @ np.abs(q).T) * np.abs(w)[None, :]).sum(axis=1), 0.0)
+    return (out, mag) if bound else out
+
+
+def order_key(f: np.ndarray) -> np.ndarray:
+    """Order-preserving uint32 key of float32 values (larger float -> larger
+    key; NaN -> 0, below everything)."""
+    u = np.ascontiguousarray(f, dtype=np.float32).view(np.uint32)
+    key = np.where(u & 0x80000000, ~u, u | 0x80000000).astype(np.uint32)
+    return np.where(np.isnan(np.asarray(f, dtype=np.float32)), np.uint32(0), key)
+
+
+def indexer_topk(logits: np.ndarray, lengths: np.ndarray, k: int) -> np.ndarray:
+    """For each row, the positions of the k largest logits among [0, len)
+    (NaN lowest, ties by smaller position), ascending; -1 padding."""
+    rows = logits.shape[0]
+    out = np.full((rows, k), -1, dtype=np.int32)
+    for r in range(rows):
+        n = int(min(max(int(lengths[r]), 0), logits.shape[1]))
+        keys = order_key(logits[r, :n].astype(np.float32)).astype(np.int64)
+        idx = np.arange(n)
+        order = np.lexsort((idx, -keys))[:k]     # key descending, position ascending
+        sel = np.sort(order)
+        out[r, :sel.size] = sel
+    return out

@@ -121,7 +121,8 @@ def test_import_does_not_touch_cuda():
                                 ("titan_mla.py", "triton_mla_sparse_attention"),
                                 ("titan_moe_align.py", "titan_moe_align_small"),
                                 ("sparse_utils.py", "triton_convert_req_index_to_global_index"),
-                                ("titan_moe_w4a16.py", "fused_moe_w4a16")):
+                                ("titan_moe_w4a16.py", "fused_moe_w4a16"),
+                                ("sparse_indexer.py", "fp8_paged_mqa_logits")):
             spec = importlib.util.spec_from_file_location("isolated_" + fname[:-3], pkg / fname)
             mod = importlib.util.module_from_spec(spec)
             spec.loader.exec_module(mod)
@@ -269,3 +270,52 @@ def test_moe_w4a16_contract_errors_on_cpu():
         repack_w4a16(torch.zeros(288, 1000, 512, dtype=torch.int32), torch.zeros(288, 1000, 128, dtype=torch.bfloat16))
     with pytest.raises(ValueError):
         repack_w4a16(torch.zeros(288, 1024, 512, dtype=torch.int32), torch.zeros(288, 1024, 64, dtype=torch.bfloat16))
+
+
+def test_indexer_host_errors():
+    import _glm53_lib
+    L = _glm53_lib.load()
+    fake = ctypes.c_void_p(0x10000)
+    mis = ctypes.c_void_p(0x10008)
+    # q, sq_t, sq_h, kv, page_bytes, bs, nb, w, sw_t, ctx, bt, bt_stride, max_blocks, T, H, D, max_len, clean, out, sl, stream
+    args = [fake, 4096, 128, fake, 64 * 132, 64, 100, fake, 32, fake, fake, 16, 16, 8, 32, 128, 1024, 1, fake, 1024, None]
+    bad = lambda i, v: L.glm53_fp8_paged_mqa_logits(*(args[:i] + [v] + args[i + 1:]))
+    assert bad(0, None) == -1
+    assert bad(15, 64) == -2        # head_dim must be 128
+    assert bad(14, 24) == -2        # heads a multiple of 16
+    assert bad(14, 80) == -2        # at most 64 heads
+    assert bad(4, 64 * 132 - 16) == -2   # page smaller than block_size x 132
+    assert bad(19, 1000) == -2      # logits row stride below max_len
+    assert bad(0, mis) == -3
+    assert bad(4, 64 * 132 + 8) == -3    # page stride not a multiple of 16
+    assert bad(13, 0) == 0          # nothing to do
+    # logits, sl, lengths, rows, max_len, k, out, so, stream
+    args = [fake, 1024, fake, 8, 1024, 512, fake, 512, None]
+    bad = lambda i, v: L.glm53_indexer_topk(*(args[:i] + [v] + args[i + 1:]))
+    assert bad(0, None) == -1
+    assert bad(5, 0) == -2
+    assert bad(5, 2048) == -2       # k above the row length
+    assert bad(7, 100) == -2        # output row stride below k
+    assert bad(3, 0) == 0
+
+
+def test_indexer_contract_errors_on_cpu():
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits, indexer_topk
+    q = torch.zeros(2, 1, 32, 128, dtype=torch.float8_e4m3fn)
+    kv = torch.zeros(10, 64, 1, 132, dtype=torch.uint8)
+    w = torch.zeros(2, 32)
+    ctx = torch.zeros(2, dtype=torch.int32)
+    bt = torch.zeros(2, 4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="q must be"):
+        fp8_paged_mqa_logits(q.float(), kv, w, ctx, bt, 256)
+    with pytest.raises(ValueError, match="kv_cache"):
+        fp8_paged_mqa_logits(q, kv[..., :128], w, ctx, bt, 256)
+    with pytest.raises(ValueError, match="weights"):
+        fp8_paged_mqa_logits(q, kv, w[:, :16], ctx, bt, 256)
+    with pytest.raises(ValueError, match="context_lens"):
+        fp8_paged_mqa_logits(q, kv, w, ctx.long(), bt, 256)
+    with pytest.raises(ValueError, match="k <="):
+        indexer_topk(torch.zeros(2, 100), ctx, 512)
+    with pytest.raises(ValueError, match="lengths"):
+        indexer_topk(torch.zeros(2, 1000), ctx.long(), 512)

@@ -1,0 +1,167 @@
+"""GPU parity of the sparse indexer decode scoring: FP8 paged MQA logits and
+the top-k pool selection, against the oracle.
+
+Tolerances.  Logits: the fp8 products are exact in fp32; the kernel sums 128
+of them per head on the matrix cores and the heads in fp32 in another order
+than the oracle's float64, so |d| <= 2^-15 * sum_h |w_h s_j| sum_d |q k|
+(a bound on fp32 accumulation error for these lengths, with margin).
+Selection: integer positions, compared exactly -- against the oracle's
+selection on the same (GPU) logits, so rounding differences in the logits
+cannot move the threshold."""
+import numpy as np
+import pytest
+
+import workloads as W
+from conftest import log_case
+
+pytestmark = pytest.mark.gpu
+
+
+def host(t):
+    import torch
+    if t.dtype == torch.float8_e4m3fn:
+        t = t.view(torch.uint8)
+    return t.cpu().numpy()
+
+
+def pages_of(cache):
+    """[num_blocks, page_bytes] uint8 view of a (possibly padded) fused cache."""
+    import torch
+    nb = cache.shape[0]
+    page = cache.stride(0)
+    flat = torch.as_strided(cache, (nb, page), (page, 1))
+    return flat.cpu().numpy()
+
+
+def check_logits(oracle, got, q, cache, w, lens, bt, max_len, clean, rows=None):
+    T = got.shape[0]
+    rows = range(T) if rows is None else rows
+    qn = host(q).reshape(T, q.shape[-2], q.shape[-1])
+    want, mag = oracle.fp8_paged_mqa_logits(qn, pages_of(cache), cache.shape[1], host(w), host(lens), host(bt),
+                                            max_len, clean=clean, bound=True)
+    g = got.cpu().numpy().astype(np.float64)
+    for t in rows:
+        n = int(min(max(int(lens[t]), 0), bt.shape[1] * cache.shape[1], max_len))
+        fin = np.isfinite(want[t, :n])
+        assert np.array_equal(np.isneginf(g[t, :n]), np.isneginf(want[t, :n])), f"row {t}: masked positions differ"
+        err = np.abs(g[t, :n][fin] - want[t, :n][fin])
+        bound = 2.0 ** -15 * mag[t, :n][fin] + 1e-30
+        assert (err <= bound).all(), f"row {t}: max err {err.max():.3e} (ratio {(err / bound).max():.2f})"
+        if clean:
+            assert np.all(np.isneginf(g[t, n:max_len]))
+
+
+@pytest.mark.parametrize("heads", [16, 32, 48, 64])
+def test_logits_small(cuda, oracle, heads):
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits
+    g = torch.Generator(device=cuda).manual_seed(100 + heads)
+    T, bs = 3, 64
+    cache, nb = W.indexer_cache(cuda, g, 3 * 1500, bs, page_pad=48)
+    perm = torch.randperm(nb, generator=g, device=cuda).to(torch.int32)
+    bt = perm[: T * (nb // T)].view(T, nb // T).contiguous()
+    bt[0, 2] = nb + 3                 # outside the cache: that page's keys are -inf
+    bt[2, 0] = -1
+    qf = torch.randn(T, 1, heads, 128, generator=g, device=cuda)
+    q = (qf * (448.0 / qf.abs().amax(dim=-1, keepdim=True))).to(torch.float8_e4m3fn)
+    w = torch.randn(T, heads, generator=g, device=cuda) / heads ** 0.5
+    lens = torch.tensor([1500, 777, 1], dtype=torch.int32, device=cuda)
+    max_len = 1600
+    for clean in (True, False):
+        log_case("indexer logits", heads, "clean", clean)
+        got = fp8_paged_mqa_logits(q, cache, w, lens, bt, max_len, clean_logits=clean)
+        torch.cuda.synchronize()
+        check_logits(oracle, got, q, cache, w, lens, bt, max_len, clean)
+
+
+def test_logits_block_sizes_and_mtp(cuda, oracle):
+    """Block sizes that split 16-key groups across pages, and next_n = 2
+    (each query row sees its own causal length)."""
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits
+    g = torch.Generator(device=cuda).manual_seed(7)
+    for bs in (8, 24, 100):
+        cache, nb = W.indexer_cache(cuda, g, 2 * 600, bs)
+        bt = torch.randperm(nb, generator=g, device=cuda).to(torch.int32)[: 2 * (nb // 2)].view(2, -1).contiguous()
+        q = (torch.randn(2, 2, 32, 128, generator=g, device=cuda) * 100).to(torch.float8_e4m3fn)
+        w = torch.randn(4, 32, generator=g, device=cuda) / 32 ** 0.5
+        lens = torch.tensor([599, 313], dtype=torch.int32, device=cuda)
+        log_case("indexer logits block", bs, "next_n 2")
+        got = fp8_paged_mqa_logits(q, cache, w, lens, bt, 640)
+        torch.cuda.synchronize()
+        rows_ctx = torch.tensor([598, 599, 312, 313], dtype=torch.int32)
+        check_logits(oracle, got, q.view(4, 1, 32, 128), cache, w, rows_ctx, bt.repeat_interleave(2, 0), 640, True)
+
+
+@pytest.fixture(scope="module")
+def decode_b8(cuda):
+    import torch
+    g = torch.Generator(device=cuda).manual_seed(W.SEED_FIXTURE)
+    log_case("indexer decode B=8 inputs (262144-token context, 65536 pools per request)")
+    return W.indexer_decode_inputs(cuda, g)
+
+
+def test_logits_full_context(cuda, oracle, decode_b8):
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits
+    q, cache, w, lens, bt, pools = decode_b8
+    log_case("indexer logits B=8 x 65536 pools")
+    got = fp8_paged_mqa_logits(q, cache, w, lens, bt, pools)
+    torch.cuda.synchronize()
+    check_logits(oracle, got, q, cache, w, lens, bt, pools, True, rows=[0, 5])
+
+
+def test_topk_matches_oracle(cuda, oracle, decode_b8):
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits, indexer_topk, indexer_decode_pool_topk
+    q, cache, w, lens, bt, pools = decode_b8
+    logits = fp8_paged_mqa_logits(q, cache, w, lens, bt, pools, clean_logits=False)
+    log_case("indexer top-512 B=8")
+    got = indexer_topk(logits, lens, 512)
+    torch.cuda.synchronize()
+    want = oracle.indexer_topk(logits.cpu().numpy(), lens.cpu().numpy(), 512)
+    assert np.array_equal(got.cpu().numpy(), want)
+    fused = indexer_decode_pool_topk(q, cache, w, lens, bt, pools)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, got)
+
+
+def test_topk_ties_specials_and_short_rows(cuda, oracle):
+    import torch
+    from sparse_indexer import indexer_topk
+    g = torch.Generator(device=cuda).manual_seed(11)
+    rows, n = 6, 70000
+    x = torch.randn(rows, n, generator=g, device=cuda)
+    x[1] = torch.randint(0, 7, (n,), generator=g, device=cuda).float()          # heavy ties
+    x[2, ::3] = float("nan")
+    x[2, 1::7] = float("-inf")
+    x[2, 5::11] = float("inf")
+    x[3] = 0.0                                                                   # all equal
+    x[4, :] = -torch.arange(n, device=cuda, dtype=torch.float32)                  # sorted descending
+    lens = torch.tensor([n, n, 65536, 40000, 512, 100], dtype=torch.int32, device=cuda)
+    for k in (512, 1, 2048):
+        log_case("indexer top-k special rows", k)
+        got = indexer_topk(x, lens, k)
+        torch.cuda.synchronize()
+        want = oracle.indexer_topk(x.cpu().numpy(), lens.cpu().numpy(), k)
+        assert np.array_equal(got.cpu().numpy(), want), k
+
+
+def test_decode_graph_replay(cuda, decode_b8):
+    import torch
+    from sparse_indexer import indexer_decode_pool_topk
+    q, cache, w, lens, bt, pools = decode_b8
+    fn = lambda: indexer_decode_pool_topk(q, cache, w, lens, bt, pools)
+    log_case("indexer decode graph replay")
+    eager = fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = fn()
+    for i in range(3):
+        captured.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager), i
+        fn()
+        torch.cuda.synchronize()

@@ -217,6 +217,57 @@ def moe_w4a16_bytes(ids: torch.Tensor, batch: int, experts=MOE_EXPERTS, hidden=M
     return distinct * per_expert + 2 * batch * hidden * 2
 
 
+# ----------------------------------------------------------------- sparse indexer (decode scoring)
+
+INDEX_HEADS = 32
+INDEX_DIM = 128
+INDEX_KPOOL = 4
+INDEX_TOPK_POOLS = 512
+
+
+def indexer_cache(device, g, num_pools, block_size=64, page_pad=0):
+    """Pool keys in DeepGEMM's fused FP8 layout: unit-normal keys quantised
+    per key to E4M3 with s = amax / 448.  Returns (cache uint8 [num_blocks,
+    block_size, 1, 132] (page stride padded by page_pad bytes), num_blocks)."""
+    nb = (num_pools + block_size - 1) // block_size
+    k = torch.randn(nb * block_size, INDEX_DIM, generator=g, device=device)
+    s = (k.abs().amax(dim=1, keepdim=True) / 448.0).clamp(min=1e-12)
+    codes = (k / s).to(torch.float8_e4m3fn).view(torch.uint8).view(nb, block_size * INDEX_DIM)
+    page = block_size * (INDEX_DIM + 4) + page_pad
+    flat = torch.zeros(nb, page, dtype=torch.uint8, device=device)
+    flat[:, : block_size * INDEX_DIM] = codes
+    flat[:, block_size * INDEX_DIM: block_size * (INDEX_DIM + 4)] = s.view(nb, block_size).contiguous().view(torch.uint8)
+    cache = torch.as_strided(flat, (nb, block_size, 1, INDEX_DIM + 4), (page, INDEX_DIM + 4, INDEX_DIM + 4, 1))
+    return cache, nb
+
+
+def indexer_decode_inputs(device, g, batch=8, context=262144, block_size=64, heads=INDEX_HEADS):
+    """Decode indexer step at the full context: each request owns
+    context / 4 pools in its own randomly placed pages.  Returns (q fp8 [B,
+    1, H, 128], cache, weights fp32 [B, H], context_lens int32 [B] (pools),
+    block_table int32 [B, max_blocks], max_model_len (pools))."""
+    pools = context // INDEX_KPOOL
+    per_req = (pools + block_size - 1) // block_size
+    cache, nb = indexer_cache(device, g, batch * pools, block_size)
+    perm = torch.randperm(nb, generator=g, device=device).to(torch.int32)
+    bt = perm[: batch * per_req].view(batch, per_req).contiguous()
+    qf = torch.randn(batch, 1, heads, INDEX_DIM, generator=g, device=device)
+    q = (qf * (448.0 / qf.abs().amax(dim=-1, keepdim=True))).to(torch.float8_e4m3fn)
+    w = torch.randn(batch, heads, generator=g, device=device) * heads ** -0.5
+    lens = torch.full((batch,), pools, dtype=torch.int32, device=device)
+    lens[1:] -= torch.randint(0, max(1, min(4096, pools // 2)), (batch - 1,), generator=g, device=device,
+                              dtype=torch.int32)
+    return q, cache, w.contiguous(), lens, bt, pools
+
+
+def indexer_bytes(lens: torch.Tensor, heads=INDEX_HEADS) -> int:
+    """Algorithmic bytes of the logits: each valid pool key (128 fp8 bytes +
+    4-byte scale) once per query, q and weights in, fp32 logits out."""
+    n = int(lens.clamp(min=0).sum().item())
+    t = lens.numel()
+    return n * (INDEX_DIM + 4) + t * heads * (INDEX_DIM + 4) + n * 4
+
+
 # ----------------------------------------------------------------- bytes
 
 def writer_bytes(n_rows: int) -> int:
