@@ -10,7 +10,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libglm53_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EXPORTED = (
     "glm53_abi_version",
@@ -32,6 +32,7 @@ EXPORTED = (
     "glm53_fused_moe_w4a16_workspace_bytes",
     "glm53_fused_moe_w4a16",
     "glm53_fp8_paged_mqa_logits",
+    "glm53_indexer_topk_workspace_bytes",
     "glm53_indexer_topk",
 )
 
@@ -94,8 +95,10 @@ def load():
     L.glm53_fp8_paged_mqa_logits.restype = I
     L.glm53_fp8_paged_mqa_logits.argtypes = [P, I64, I64, P, I64, I64, I64, P, I64, P, P, I64, I64, I64, I64,
                                              I64, I64, I, P, I64, P]
+    L.glm53_indexer_topk_workspace_bytes.restype = I64
+    L.glm53_indexer_topk_workspace_bytes.argtypes = [I64, I64, I64]
     L.glm53_indexer_topk.restype = I
-    L.glm53_indexer_topk.argtypes = [P, I64, P, I64, I64, I64, P, I64, P]
+    L.glm53_indexer_topk.argtypes = [P, I64, P, I64, I64, I64, P, I64, P, I64, P]
     version = L.glm53_abi_version()
     if version != ABI_VERSION:
         raise ImportError(f"{LIB_PATH} has ABI version {version}, expected {ABI_VERSION}")

@@ -27,11 +27,16 @@
 // k-slot 8g + e of MFMA m is dim 32g + 8m + e on both sides.  A wave issues
 // the loads of all its groups before the first MFMA.
 //
-// Top-k kernel: one 1024-thread workgroup per row; radix select on the
-// order-preserving 32-bit keys of the logits (12, 12 and 8 bits, a 4096-bin
-// LDS histogram per pass) finds the k-th largest key, then one ordered
-// compaction writes the selected positions in ascending order (ties at the
-// threshold resolved by position): deterministic.
+// Top-k: order-preserving 32-bit keys, radix select with 12-, 12- and 8-bit
+// digits (LDS histograms) for the k-th largest key, then an ordered
+// compaction (two workgroup scans) that writes the selected positions in
+// ascending order, ties at the threshold resolved by position:
+// deterministic.  One workgroup per row is bound by its CU's vector rate, so
+// long rows run in two stages: workgroups (row, chunk) keep each chunk's
+// local top-k in position order (a key of the row's top k is in its chunk's
+// top k), then one workgroup per row selects from those candidates.  Keys
+// stay in registers (thread-contiguous runs of positions) through every
+// pass; rows too long for the two stages are re-read from L2 per pass.
 #include "glm53_common.h"
 
 namespace glm53 {
@@ -173,8 +178,12 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
 }
 
 // ------------------------------------------------------------------ top-k
-constexpr int kTopkThreads = 1024;
 constexpr int kHistBins = 4096;
+constexpr int kChunkThreads = 512;
+constexpr int kFinalThreads = 1024;
+constexpr int kSweepThreads = 1024;
+constexpr int kSweepKeys = 32;                      // keys per thread per sweep
+constexpr int kSweep = kSweepThreads * kSweepKeys;  // positions per sweep (32768)
 
 struct TopkArgs {
   const float* logits;      // [rows][*], row stride sl
@@ -184,116 +193,372 @@ struct TopkArgs {
   int k;
   int32_t* out;             // [rows][k], row stride so
   int64_t so;
+  uint32_t* cand_key;       // [rows][chunks * k] chunk-local top-k keys, in position order
+  int32_t* cand_pos;        // [rows][chunks * k] their positions
+  int chunks;
+  int chunk_len;
 };
 
+// Order-preserving key: a larger float has a larger key; NaN -> 0, below
+// everything else (-inf is 0x007FFFFF).  Positions past the row's length
+// also get key 0: with more valid positions than k they are never reached,
+// and at equal keys a smaller position always wins.
 __device__ __forceinline__ uint32_t order_key(float f) {
   const uint32_t u = __float_as_uint(f);
-  if (f != f) return 0u;                                   // NaN ranks last
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);      // larger float -> larger key
+  if (f != f) return 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-struct TopkShared {
-  uint32_t hist[kHistBins];
-  uint32_t scan[kTopkThreads];
-  uint32_t scan2[kTopkThreads];
-  uint32_t pick[2];   // digit, count of keys above it
+template <int kThreads>
+struct SelShared {
+  __attribute__((aligned(16))) uint32_t hist[2][kHistBins];   // passes alternate, so a pass clears the one after next
+  uint32_t wsum[kThreads / 64];
+  uint32_t wmin[kThreads / 64];
+  uint32_t wmax[kThreads / 64];
+  uint32_t pick[3];              // digit, keys above it, keys in it
 };
 
-// Inclusive prefix sum over the workgroup of one value per thread (Hillis-Steele in LDS).
-__device__ uint32_t block_inclusive_scan(uint32_t* buf, uint32_t v) {
-  const int tid = threadIdx.x;
-  buf[tid] = v;
-  __syncthreads();
-  for (int off = 1; off < kTopkThreads; off <<= 1) {
-    const uint32_t add = tid >= off ? buf[tid - off] : 0u;
-    __syncthreads();
-    buf[tid] += add;
-    __syncthreads();
-  }
-  return buf[tid];
+// Inclusive scan of one value per lane within the wave: row_shr 1, 2, 4, 8
+// inside rows of 16 lanes, then row_bcast 15 and 31 carry row totals upward.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), kCtrl, kRowMask, 0xf, false));
 }
 
-__global__ __launch_bounds__(kTopkThreads) void indexer_topk_kernel(const TopkArgs a) {
-  __shared__ TopkShared sh;
-  const int row = blockIdx.x;
-  const int tid = threadIdx.x;
-  int len = a.lengths[row];
-  len = len < 0 ? 0 : len > a.max_len ? a.max_len : len;
-  const float* x = a.logits + row * a.sl;
-  int32_t* out = a.out + row * a.so;
-  const int k = a.k;
-  if (len <= k) {   // every valid position is selected (uniform)
-    for (int i = tid; i < k; i += kTopkThreads) out[i] = i < len ? i : -1;
-    return;
-  }
-  // Thread tid owns the contiguous positions [lo, hi).
-  const int seg = (len + kTopkThreads - 1) / kTopkThreads;
-  const int lo = tid * seg < len ? tid * seg : len;
-  const int hi = lo + seg < len ? lo + seg : len;
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += dpp_or_zero<0x111, 0xf>(v);
+  v += dpp_or_zero<0x112, 0xf>(v);
+  v += dpp_or_zero<0x114, 0xf>(v);
+  v += dpp_or_zero<0x118, 0xf>(v);
+  v += dpp_or_zero<0x142, 0xa>(v);
+  v += dpp_or_zero<0x143, 0xc>(v);
+  return v;
+}
 
-  uint32_t prefix = 0, pmask = 0;
-  uint32_t need = static_cast<uint32_t>(k);   // keys still to take at or below the current prefix
-  const int shifts[3] = {20, 8, 0};
-  const int widths[3] = {12, 12, 8};
+// Largest value of the wave (broadcast).
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) {
+  v = max(v, dpp_or_zero<0x111, 0xf>(v));
+  v = max(v, dpp_or_zero<0x112, 0xf>(v));
+  v = max(v, dpp_or_zero<0x114, 0xf>(v));
+  v = max(v, dpp_or_zero<0x118, 0xf>(v));
+  v = max(v, dpp_or_zero<0x142, 0xa>(v));
+  v = max(v, dpp_or_zero<0x143, 0xc>(v));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+// Exclusive scan over the workgroup of one value per thread; *total gets the
+// sum.  sh.wsum is read after the return: a barrier must separate the
+// return from the next scan.
+template <int kThreads>
+__device__ __forceinline__ uint32_t block_excl_scan(SelShared<kThreads>& sh, uint32_t v, uint32_t* total) {
+  constexpr int kWaves = kThreads / 64;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t incl = wave_incl_scan(v);
+  if (lane == 63) sh.wsum[w] = incl;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
 #pragma unroll
-  for (int pass = 0; pass < 3; pass++) {
-    const int shift = shifts[pass];
-    const uint32_t dmask = (1u << widths[pass]) - 1u;
-    const int nbins = 1 << widths[pass];
-    for (int b = tid; b < kHistBins; b += kTopkThreads) sh.hist[b] = 0u;
+  for (int i = 0; i < kWaves; i++) {
+    const uint32_t t = sh.wsum[i];
+    before += i < w ? t : 0u;
+    all += t;
+  }
+  *total = all;
+  return before + incl - v;
+}
+
+// Selection threshold: keys whose bits under pmask exceed thr are all in the
+// top k; of the keys equal to thr under pmask the first `need` (by index)
+// are.  pmask is all ones unless a pass found that a whole digit bin is
+// taken, which ends the search early.
+struct Threshold {
+  uint32_t thr, pmask, need;
+};
+
+// Radix select of the k-th largest key with LDS histograms of up to 12-bit
+// digits, starting below the bits that kmin and kmax (this thread's smallest
+// and largest key, over keys that must count) share across the workgroup: a
+// concentrated set of keys (a chunk's candidates) still spreads over the
+// bins, which keeps the histogram atomics from piling onto a few addresses.
+// for_keys(f) calls f(key) for every key of this thread; the keys matching
+// the shared bits must number at least k.
+template <int kThreads, class ForKeys>
+__device__ Threshold radix_threshold(SelShared<kThreads>& sh, ForKeys for_keys, uint32_t k, uint32_t kmin,
+                                     uint32_t kmax) {
+  constexpr int kWaves = kThreads / 64;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  kmin = ~wave_max(~kmin);
+  kmax = wave_max(kmax);
+  if (lane == 0) { sh.wmin[w] = kmin; sh.wmax[w] = kmax; }
+  for (int b = tid; b < 2 * kHistBins; b += kThreads) (&sh.hist[0][0])[b] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kWaves; i++) { kmin = min(kmin, sh.wmin[i]); kmax = max(kmax, sh.wmax[i]); }
+  const uint32_t diff = kmin ^ kmax;
+  if (diff == 0) return {kmax, ~0u, k};   // one distinct key
+  int top = 32 - __clz(static_cast<int>(diff));   // bits [top, 32) are shared
+  uint32_t pmask = top == 32 ? 0u : ~((1u << top) - 1u);
+  uint32_t prefix = kmax & pmask, need = k;
+  for (int pass = 0; top > 0; pass++) {
+    const int width = top < 12 ? top : 12;
+    const int shift = top - width;
+    top = shift;
+    const int nb = 1 << width;
+    const uint32_t dmask = static_cast<uint32_t>(nb - 1);
+    uint32_t* hist = sh.hist[pass & 1];
+    for_keys([&](uint32_t key) {
+      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & dmask], 1u);
+    });
+    if (pass == 1)   // pass 0's histogram is no longer read: clear it for pass 2
+      for (int b = tid; b < kHistBins; b += kThreads) sh.hist[0][b] = 0u;
     __syncthreads();
-    for (int i = lo; i < hi; i++) {
-      const uint32_t key = order_key(x[i]);
-      if ((key & pmask) == prefix) atomicAdd(&sh.hist[(key >> shift) & dmask], 1u);
-    }
-    __syncthreads();
-    // Suffix counts: thread tid owns bins [bpt*(T-1-tid), ...) so that an
-    // inclusive scan over tid counts keys in the highest bins first.
-    const int bpt = nbins / kTopkThreads > 0 ? nbins / kTopkThreads : 1;
-    const int b0 = nbins - bpt * (tid + 1);   // this thread's lowest bin (bins above it belong to lower tids)
+    // Thread tid owns bpt bins counted from the top: the keys in higher bins
+    // are the wave totals of lower waves plus the lanes below in this wave.
+    const int bpt = nb >= kThreads ? nb / kThreads : 1;
+    const int b0 = nb - bpt * (tid + 1);
     uint32_t mine = 0;
-    if (b0 >= 0)
-      for (int b = b0; b < b0 + bpt; b++) mine += sh.hist[b];
-    const uint32_t incl = block_inclusive_scan(sh.scan, mine);
-    const uint32_t excl = incl - mine;        // keys in bins above this thread's range
-    if (b0 >= 0 && excl < need && incl >= need) {
+    if (b0 >= 0) {
+      if ((bpt & 3) == 0) {
+        for (int b = b0; b < b0 + bpt; b += 4) {
+          const uint4 v = *reinterpret_cast<const uint4*>(hist + b);
+          mine += v.x + v.y + v.z + v.w;
+        }
+      } else {
+        for (int b = b0; b < b0 + bpt; b++) mine += hist[b];
+      }
+    }
+    const uint32_t incl = wave_incl_scan(mine);
+    if (lane == 63) sh.wsum[w] = incl;
+    __syncthreads();
+    uint32_t excl = incl - mine;
+#pragma unroll
+    for (int i = 0; i < kWaves; i++) excl += i < w ? sh.wsum[i] : 0u;
+    if (b0 >= 0 && excl < need && excl + mine >= need) {
       uint32_t above = excl;
       for (int b = b0 + bpt - 1; b >= b0; b--) {
-        if (above + sh.hist[b] >= need) {
+        const uint32_t h = hist[b];
+        if (above + h >= need) {
           sh.pick[0] = static_cast<uint32_t>(b);
           sh.pick[1] = above;
+          sh.pick[2] = h;
           break;
         }
-        above += sh.hist[b];
+        above += h;
       }
     }
     __syncthreads();
     prefix |= sh.pick[0] << shift;
     pmask |= dmask << shift;
     need -= sh.pick[1];
-    __syncthreads();
+    if (sh.pick[2] == need) break;   // the whole bin is taken (uniform)
   }
-  // prefix = the k-th largest key; take every key above it and the first
-  // `need` keys equal to it, in position order.
-  uint32_t gt = 0, eq = 0;
-  for (int i = lo; i < hi; i++) {
-    const uint32_t key = order_key(x[i]);
-    gt += key > prefix;
-    eq += key == prefix;
+  return {prefix, pmask, need};
+}
+
+// Ordered compaction of the keys kk of this thread, which hold workgroup
+// indices base + [0, P) (thread-contiguous): the keys above the threshold and
+// the first `need` keys at it, counting from eq_seen keys at it already seen
+// at lower indices outside the workgroup's keys; emit(o, j) is called with
+// the output rank o (from written) of key j.  Returns the keys at the
+// threshold and the keys selected in *n_eq, *n_sel.  Counts must stay below
+// 65536 per workgroup (they are packed in one scan).
+template <int kThreads, int P, class Emit>
+__device__ void emit_selected(SelShared<kThreads>& sh, const uint32_t (&kk)[P], const Threshold& t,
+                              uint32_t eq_seen, uint32_t written, Emit emit, uint32_t* n_eq, uint32_t* n_sel) {
+  uint32_t ngt = 0, neq = 0;
+#pragma unroll
+  for (int j = 0; j < P; j++) {
+    const uint32_t m = kk[j] & t.pmask;
+    ngt += m > t.thr;
+    neq += m == t.thr;
   }
-  const uint32_t eq_incl = block_inclusive_scan(sh.scan, eq);
-  const uint32_t eq_before = eq_incl - eq;
-  const uint32_t eq_take = eq_before >= need ? 0u : (need - eq_before < eq ? need - eq_before : eq);
-  const uint32_t sel = gt + eq_take;
-  const uint32_t sel_incl = block_inclusive_scan(sh.scan2, sel);
-  uint32_t pos = sel_incl - sel;
-  uint32_t eq_left = eq_take;
-  for (int i = lo; i < hi; i++) {
-    const uint32_t key = order_key(x[i]);
-    if (key > prefix || (key == prefix && eq_left > 0)) {
-      if (key == prefix) eq_left--;
-      out[pos++] = i;
+  uint32_t tot;
+  const uint32_t ex = block_excl_scan(sh, (ngt << 16) | neq, &tot);
+  const uint32_t taken_before = eq_seen < t.need ? eq_seen : t.need;
+  const uint32_t eq_tot = eq_seen + (tot & 0xffffu);
+  *n_eq = tot & 0xffffu;
+  *n_sel = (tot >> 16) + (eq_tot < t.need ? eq_tot : t.need) - taken_before;
+  uint32_t r = eq_seen + (ex & 0xffffu);
+  uint32_t o = written + (ex >> 16) + (r < t.need ? r : t.need) - taken_before;
+  if (ngt + neq == 0) return;
+#pragma unroll
+  for (int j = 0; j < P; j++) {
+    const uint32_t m = kk[j] & t.pmask;
+    const bool eq = m == t.thr;
+    if (m > t.thr || (eq && r < t.need)) emit(o++, j);
+    r += eq;
+  }
+}
+
+// Keys of row positions i0 + [0, P) (P a multiple of 4, i0 a multiple of 4,
+// x 16-byte aligned); positions at or past n get key 0.
+template <int P>
+__device__ __forceinline__ void load_row_keys(const float* x, int n, int i0, uint32_t (&kk)[P]) {
+#pragma unroll
+  for (int q = 0; q < P / 4; q++) {
+    const int p = i0 + 4 * q;
+    if (p + 3 < n) {
+      const float4 v = *reinterpret_cast<const float4*>(x + p);
+      kk[4 * q] = order_key(v.x); kk[4 * q + 1] = order_key(v.y);
+      kk[4 * q + 2] = order_key(v.z); kk[4 * q + 3] = order_key(v.w);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) kk[4 * q + e] = p + e < n ? order_key(x[p + e]) : 0u;
     }
+  }
+}
+
+template <int P, class F>
+__device__ __forceinline__ void for_each_key(const uint32_t (&kk)[P], F&& f) {
+#pragma unroll
+  for (int j = 0; j < P; j++) f(kk[j]);
+}
+
+__device__ __forceinline__ int clamp_len(const TopkArgs& a, int row) {
+  const int len = a.lengths[row];
+  return len < 0 ? 0 : len > a.max_len ? a.max_len : len;
+}
+
+// Chunk stage: workgroup (row, chunk c) keeps the local top-k of positions
+// [c * chunk_len, (c + 1) * chunk_len) of the row, in position order, as
+// candidates (every valid position when the chunk holds at most k).  A key of
+// the row's top k is in its chunk's top k, so the candidates hold the answer.
+template <int P>
+__global__ __launch_bounds__(kChunkThreads) void topk_chunk_kernel(const TopkArgs a) {
+  __shared__ SelShared<kChunkThreads> sh;
+  const int row = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+  const int len = clamp_len(a, row);
+  const int k = a.k;
+  const int start = c * a.chunk_len;
+  const int rest = len - start;
+  const int valid = rest < 0 ? 0 : rest > a.chunk_len ? a.chunk_len : rest;
+  if (len <= k || valid == 0) return;   // uniform
+  uint32_t kk[P];
+  load_row_keys<P>(a.logits + row * a.sl + start, valid, tid * P, kk);
+  const int64_t cb = (static_cast<int64_t>(row) * a.chunks + c) * k;
+  uint32_t* ck = a.cand_key + cb;
+  int32_t* cp = a.cand_pos + cb;
+  if (valid <= k) {
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+      const int i = tid * P + j;
+      if (i < valid) { ck[i] = kk[j]; cp[i] = start + i; }
+    }
+    return;
+  }
+  uint32_t kmin = ~0u, kmax = 0u;
+#pragma unroll
+  for (int j = 0; j < P; j++)
+    if (tid * P + j < valid) { kmin = min(kmin, kk[j]); kmax = max(kmax, kk[j]); }
+  const Threshold t = radix_threshold(sh, [&](auto f) { for_each_key(kk, f); }, static_cast<uint32_t>(k), kmin, kmax);
+  uint32_t n_eq, n_sel;
+  emit_selected(sh, kk, t, 0u, 0u, [&](uint32_t o, int j) {
+    if (o < static_cast<uint32_t>(k)) { ck[o] = kk[j]; cp[o] = start + tid * P + j; }
+  }, &n_eq, &n_sel);
+}
+
+// Final stage: one workgroup per row selects the top k, in position order,
+// from the row itself (kCand false: row length at most kFinalThreads * P) or
+// from the chunk stage's candidates (chunk-major, so in position order too).
+// Candidate slot s of chunk c is filled when s < min(k, valid positions of
+// the chunk); the chunk length exceeds k, so only the last chunk holding
+// valid positions can be short and every empty slot (key 0) follows every
+// filled one: never selected.
+template <int P, bool kCand>
+__global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(const TopkArgs a) {
+  __shared__ SelShared<kFinalThreads> sh;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int len = clamp_len(a, row);
+  const int k = a.k;
+  int32_t* out = a.out + row * a.so;
+  if (len <= k) {   // every valid position is selected (uniform)
+    for (int i = tid; i < k; i += kFinalThreads) out[i] = i < len ? i : -1;
+    return;
+  }
+  uint32_t kk[P];
+  int32_t pos[kCand ? P : 1];
+  uint32_t kmin = ~0u, kmax = 0u;
+  const int64_t cb = kCand ? static_cast<int64_t>(row) * a.chunks * k : 0;
+  if (kCand) {
+    // Candidate i = tid * P + j is slot sl of chunk c (i = c * k + sl).  The
+    // loads are unconditional (issued together), from clamped indices when
+    // k is not a multiple of 4, else as 4-candidate vectors (a vector never
+    // straddles chunks then); filled slots are picked afterwards.
+    const int n_cand = a.chunks * k;
+    if ((k & 3) == 0) {
+#pragma unroll
+      for (int q = 0; q < P / 4; q++) {
+        const int i = tid * P + 4 * q < n_cand ? tid * P + 4 * q : n_cand - 4;
+        const uint4 kv = *reinterpret_cast<const uint4*>(a.cand_key + cb + i);
+        const int4 pv = *reinterpret_cast<const int4*>(a.cand_pos + cb + i);
+        kk[4 * q] = kv.x; kk[4 * q + 1] = kv.y; kk[4 * q + 2] = kv.z; kk[4 * q + 3] = kv.w;
+        pos[4 * q] = pv.x; pos[4 * q + 1] = pv.y; pos[4 * q + 2] = pv.z; pos[4 * q + 3] = pv.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < P; j++) {
+        const int i = tid * P + j < n_cand ? tid * P + j : n_cand - 1;
+        kk[j] = a.cand_key[cb + i];
+        pos[j] = a.cand_pos[cb + i];
+      }
+    }
+    int c = (tid * P) / k, sl = tid * P - c * k;
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+      const int rest = len - c * a.chunk_len;
+      const int n_c = rest < 0 ? 0 : rest > k ? k : rest;
+      const bool ok = c < a.chunks && sl < n_c;
+      kk[j] = ok ? kk[j] : 0u;
+      if (ok) { kmin = min(kmin, kk[j]); kmax = max(kmax, kk[j]); }
+      if (++sl == k) { sl = 0; c++; }
+    }
+  } else {
+    load_row_keys<P>(a.logits + row * a.sl, len, tid * P, kk);
+#pragma unroll
+    for (int j = 0; j < P; j++)
+      if (tid * P + j < len) { kmin = min(kmin, kk[j]); kmax = max(kmax, kk[j]); }
+  }
+  const Threshold t = radix_threshold(sh, [&](auto f) { for_each_key(kk, f); }, static_cast<uint32_t>(k), kmin, kmax);
+  uint32_t n_eq, n_sel;
+  emit_selected(sh, kk, t, 0u, 0u, [&](uint32_t o, int j) {
+    if (o < static_cast<uint32_t>(k)) out[o] = kCand ? pos[kCand ? j : 0] : tid * P + j;
+  }, &n_eq, &n_sel);
+}
+
+// Rows too long for the two stages: one workgroup per row re-reads the row
+// (from L2) in sweeps of 32768 positions for each radix pass and for the
+// compaction, which carries its counts from sweep to sweep.
+__global__ __launch_bounds__(kSweepThreads) void topk_sweep_kernel(const TopkArgs a) {
+  __shared__ SelShared<kSweepThreads> sh;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const int len = clamp_len(a, row);
+  const int k = a.k;
+  int32_t* out = a.out + row * a.so;
+  if (len <= k) {
+    for (int i = tid; i < k; i += kSweepThreads) out[i] = i < len ? i : -1;
+    return;
+  }
+  const float* x = a.logits + row * a.sl;
+  const int sweeps = (len + kSweep - 1) / kSweep;
+  const Threshold t = radix_threshold(sh, [&](auto f) {
+    for (int sw = 0; sw < sweeps; sw++) {
+      uint32_t kk[kSweepKeys];
+      load_row_keys<kSweepKeys>(x + sw * kSweep, len - sw * kSweep, tid * kSweepKeys, kk);
+      for_each_key(kk, f);
+    }
+  }, static_cast<uint32_t>(k), 0u, ~0u);
+  uint32_t eq_seen = 0, written = 0;
+  for (int sw = 0; sw < sweeps; sw++) {
+    uint32_t kk[kSweepKeys];
+    const int base = sw * kSweep;
+    load_row_keys<kSweepKeys>(x + base, len - base, tid * kSweepKeys, kk);
+    uint32_t n_eq, n_sel;
+    emit_selected(sh, kk, t, eq_seen, written, [&](uint32_t o, int j) {
+      if (o < static_cast<uint32_t>(k)) out[o] = base + tid * kSweepKeys + j;
+    }, &n_eq, &n_sel);
+    eq_seen += n_eq;
+    written += n_sel;
+    __syncthreads();   // the next sweep's scan rewrites sh.wsum
   }
 }
 
@@ -341,16 +606,106 @@ extern "C" int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t s
   return static_cast<int>(hipGetLastError());
 }
 
+namespace {
+
+// How the top-k of rows of max_len columns runs: one final workgroup over
+// the row (direct, P keys per thread), or the chunk stage (chunks of
+// 512 * chunk_p positions, chunk_len > k) then the final stage over
+// chunks * k candidates, or the sweep kernel.  Among chunk sizes the one with
+// the fewest keys per thread over the two stages wins.
+struct TopkPlan {
+  enum Mode { kDirect, kChunked, kSweepMode } mode;
+  int chunk_p, final_p, chunks, chunk_len;
+};
+
+int final_p_for(int64_t n) {
+  for (int p : {4, 8, 16, 32})
+    if (n <= int64_t(kFinalThreads) * p) return p;
+  return 0;
+}
+
+TopkPlan plan_topk(int64_t max_len, int64_t k) {
+  if (max_len <= int64_t(kFinalThreads) * 4) return {TopkPlan::kDirect, 0, 4, 0, 0};
+  TopkPlan best{TopkPlan::kSweepMode, 0, 0, 0, 0};
+  int best_cost = 1 << 30;
+  for (int p : {8, 16, 32}) {
+    const int64_t len_c = int64_t(kChunkThreads) * p;
+    if (len_c <= k) continue;
+    const int64_t chunks = (max_len + len_c - 1) / len_c;
+    if (chunks < 2) continue;
+    const int fp = final_p_for(chunks * k);
+    if (fp == 0) continue;
+    if (p + fp < best_cost) {
+      best_cost = p + fp;
+      best = {TopkPlan::kChunked, p, fp, static_cast<int>(chunks), static_cast<int>(len_c)};
+    }
+  }
+  if (best.mode == TopkPlan::kSweepMode) {
+    const int fp = final_p_for(max_len);
+    if (fp) return {TopkPlan::kDirect, 0, fp, 0, 0};
+  }
+  return best;
+}
+
+int64_t topk_ws_bytes(const TopkPlan& p, int64_t rows, int64_t k) {
+  if (p.mode != TopkPlan::kChunked) return 0;
+  return (rows * p.chunks * k * 8 + 255) / 256 * 256;
+}
+
+bool topk_shape_ok(int64_t num_rows, int64_t max_len, int64_t k) {
+  return num_rows >= 0 && num_rows <= (int64_t(1) << 30) && k >= 1 && k <= max_len && max_len <= (int64_t(1) << 30);
+}
+
+template <int P>
+void launch_final(bool cand, dim3 grid, hipStream_t st, const TopkArgs& a) {
+  void (*kernel)(TopkArgs) = cand ? topk_final_kernel<P, true> : topk_final_kernel<P, false>;
+  hipLaunchKernelGGL(kernel, grid, dim3(kFinalThreads), 0, st, a);
+}
+
+}  // namespace
+
+extern "C" int64_t glm53_indexer_topk_workspace_bytes(int64_t num_rows, int64_t max_len, int64_t k) {
+  if (!topk_shape_ok(num_rows, max_len, k)) return 0;
+  return topk_ws_bytes(plan_topk(max_len, k), num_rows, k);
+}
+
 extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t* lengths, int64_t num_rows,
-                                  int64_t max_len, int64_t k, int32_t* out, int64_t so, void* stream) {
+                                  int64_t max_len, int64_t k, void* workspace, int64_t workspace_bytes,
+                                  int32_t* out, int64_t so, void* stream) {
   if (!logits || !lengths || !out) return GLM53_ERR_NULL_POINTER;
-  if (num_rows < 0 || num_rows > (1 << 30) || k < 1 || k > max_len || max_len > (int64_t(1) << 30) ||
-      sl < max_len || so < k)
-    return GLM53_ERR_BAD_SHAPE;
+  if (!topk_shape_ok(num_rows, max_len, k) || sl < max_len || so < k) return GLM53_ERR_BAD_SHAPE;
   if (num_rows == 0) return 0;
-  TopkArgs a{logits, sl, lengths, static_cast<int>(max_len), static_cast<int>(k), out, so};
+  if (!aligned(logits, 16) || sl % 4) return GLM53_ERR_MISALIGNED;
+  const TopkPlan plan = plan_topk(max_len, k);
+  const int64_t need = topk_ws_bytes(plan, num_rows, k);
+  if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 16))) return GLM53_ERR_WORKSPACE;
+  TopkArgs a{logits, sl, lengths, static_cast<int>(max_len), static_cast<int>(k), out, so, nullptr, nullptr,
+             plan.chunks, plan.chunk_len};
+  if (need) {
+    a.cand_key = static_cast<uint32_t*>(workspace);
+    a.cand_pos = reinterpret_cast<int32_t*>(a.cand_key + num_rows * plan.chunks * k);
+  }
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 rows_grid(static_cast<unsigned>(num_rows));
   (void)hipGetLastError();
-  hipLaunchKernelGGL(indexer_topk_kernel, dim3(static_cast<unsigned>(num_rows)), dim3(kTopkThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
+  if (plan.mode == TopkPlan::kSweepMode) {
+    hipLaunchKernelGGL(topk_sweep_kernel, rows_grid, dim3(kSweepThreads), 0, st, a);
+    return static_cast<int>(hipGetLastError());
+  }
+  const bool cand = plan.mode == TopkPlan::kChunked;
+  if (cand) {
+    const dim3 grid(static_cast<unsigned>(num_rows), static_cast<unsigned>(plan.chunks));
+    switch (plan.chunk_p) {
+      case 8: hipLaunchKernelGGL(topk_chunk_kernel<8>, grid, dim3(kChunkThreads), 0, st, a); break;
+      case 16: hipLaunchKernelGGL(topk_chunk_kernel<16>, grid, dim3(kChunkThreads), 0, st, a); break;
+      default: hipLaunchKernelGGL(topk_chunk_kernel<32>, grid, dim3(kChunkThreads), 0, st, a); break;
+    }
+  }
+  switch (plan.final_p) {
+    case 4: launch_final<4>(cand, rows_grid, st, a); break;
+    case 8: launch_final<8>(cand, rows_grid, st, a); break;
+    case 16: launch_final<16>(cand, rows_grid, st, a); break;
+    default: launch_final<32>(cand, rows_grid, st, a); break;
+  }
   return static_cast<int>(hipGetLastError());
 }

@@ -95,9 +95,12 @@ def indexer_topk(logits: torch.Tensor, lengths: torch.Tensor, k: int = 512) -> t
     if rows == 0:
         return out
     L = _lib.load()
+    ws_bytes = int(L.glm53_indexer_topk_workspace_bytes(rows, n, k))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=logits.device)
     with torch.cuda.device(logits.device):
         rc = L.glm53_indexer_topk(logits.data_ptr(), logits.stride(0), lengths.contiguous().data_ptr(), rows, n, k,
-                                  out.data_ptr(), out.stride(0), _lib.stream_handle(logits.device))
+                                  ws.data_ptr(), ws_bytes, out.data_ptr(), out.stride(0),
+                                  _lib.stream_handle(logits.device))
     _lib.check(rc, "glm53_indexer_topk")
     return out
 

@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define GLM53_ABI_VERSION 1
+#define GLM53_ABI_VERSION 2
 
 /* Argument errors (negative return codes). */
 #define GLM53_ERR_NULL_POINTER   (-1)
@@ -325,12 +325,20 @@ int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t sq_h,
  * Top-k per row of the indexer logits: the top-512 pool selection whose pool
  * ids (topk_dst / pool_topk) the kpool expansion consumes
  * (integration/patch_indexer_sharding.py:58-79,
- * integration/patch_decode_indexer.py:64-72; vLLM's radix top-k): the k largest of logits[r, 0 : lengths[r]] (NaN ranks
- * lowest, ties by smaller position), written as positions in ascending order;
- * a row with fewer than k valid positions gets all of them, then -1.
+ * integration/patch_decode_indexer.py:64-72; vLLM's radix top-k): the k
+ * largest of logits[r, 0 : lengths[r]] (lengths clamped to [0, max_len]; NaN
+ * ranks lowest, ties by smaller position), written as positions in ascending
+ * order; a row with fewer than k valid positions gets all of them, then -1.
+ *   logits     fp32 [num_rows][max_len], row stride sl (16-byte aligned, sl % 4 == 0)
+ *   workspace  device scratch of glm53_indexer_topk_workspace_bytes(...) bytes
+ *              (0 for rows of at most 4096 columns; may then be NULL)
+ *   out        int32 [num_rows][k], row stride so
  */
+int64_t glm53_indexer_topk_workspace_bytes(int64_t num_rows, int64_t max_len,
+                                           int64_t k);
 int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t* lengths,
                        int64_t num_rows, int64_t max_len, int64_t k,
+                       void* workspace, int64_t workspace_bytes,
                        int32_t* out, int64_t so, void* stream);
 
 #ifdef __cplusplus

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_glm53_lib.EXPORTED)
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.glm53_abi_version() == 1
+    assert lib.glm53_abi_version() == 2
 
 
 def test_host_side_argument_errors():
@@ -289,14 +289,26 @@ def test_indexer_host_errors():
     assert bad(0, mis) == -3
     assert bad(4, 64 * 132 + 8) == -3    # page stride not a multiple of 16
     assert bad(13, 0) == 0          # nothing to do
-    # logits, sl, lengths, rows, max_len, k, out, so, stream
-    args = [fake, 1024, fake, 8, 1024, 512, fake, 512, None]
+    # logits, sl, lengths, rows, max_len, k, ws, ws_bytes, out, so, stream
+    args = [fake, 1024, fake, 8, 1024, 512, None, 0, fake, 512, None]
     bad = lambda i, v: L.glm53_indexer_topk(*(args[:i] + [v] + args[i + 1:]))
     assert bad(0, None) == -1
     assert bad(5, 0) == -2
     assert bad(5, 2048) == -2       # k above the row length
-    assert bad(7, 100) == -2        # output row stride below k
+    assert bad(9, 100) == -2        # output row stride below k
+    assert bad(1, 1026) == -3       # row stride not a multiple of 4 floats
     assert bad(3, 0) == 0
+    # long rows run in two stages and need the candidates' workspace
+    ws = L.glm53_indexer_topk_workspace_bytes
+    assert ws(8, 4096, 512) == 0
+    assert ws(8, 65536, 512) == 8 * 16 * 512 * 8          # 16 chunks of 4096, key + position per candidate
+    assert ws(8, 65536, 2048) == 8 * 8 * 2048 * 8         # 8 chunks of 8192
+    assert ws(2, 140000, 4096) == 0                       # too many candidates: single-workgroup sweeps
+    assert ws(8, 65536, 0) == 0 and ws(-1, 65536, 512) == 0
+    big = [fake, 65536, fake, 8, 65536, 512, None, 0, fake, 512, None]
+    assert L.glm53_indexer_topk(*big) == -4
+    big[6], big[7] = fake, ws(8, 65536, 512) - 1
+    assert L.glm53_indexer_topk(*big) == -4
 
 
 def test_indexer_contract_errors_on_cpu():

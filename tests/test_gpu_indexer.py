@@ -147,6 +147,34 @@ def test_topk_ties_specials_and_short_rows(cuda, oracle):
         assert np.array_equal(got.cpu().numpy(), want), k
 
 
+@pytest.mark.parametrize("n,k", [
+    (4096, 512),      # one workgroup over the row, 4 keys per thread
+    (32768, 16384),   # one workgroup over the row, 32 keys per thread (chunks would not exceed k)
+    (65536, 512),     # chunks of 4096, 8192 candidates
+    (20000, 8192),    # chunks of 16384, 16384 candidates
+    (140000, 4096),   # too many candidates: sweeps over the row
+])
+def test_topk_every_plan(cuda, oracle, n, k):
+    """Each execution plan of the top-k, with ragged, clamped, tied and NaN
+    rows; chunk boundaries at 4096, 8192 and 16384 positions."""
+    import torch
+    from sparse_indexer import indexer_topk
+    g = torch.Generator(device=cuda).manual_seed(n + k)
+    lens_list = [n, n - 1, min(n, 4097), min(n, 8193), min(n, 16385), k + 1, k, 3, -5, n + 1000]
+    rows = len(lens_list)
+    x = torch.randn(rows, n, generator=g, device=cuda)
+    x[1] = torch.randint(0, 3, (n,), generator=g, device=cuda).float()     # heavy ties
+    x[2, ::2] = float("nan")
+    x[3] = 1.0                                                              # all equal
+    x[4, :] = torch.arange(n, device=cuda, dtype=torch.float32)             # ascending: the tail wins
+    lens = torch.tensor(lens_list, dtype=torch.int32, device=cuda)
+    log_case("indexer top-k plan", n, k)
+    got = indexer_topk(x, lens, k)
+    torch.cuda.synchronize()
+    want = oracle.indexer_topk(x.cpu().numpy(), np.clip(lens.cpu().numpy(), 0, n), k)
+    assert np.array_equal(got.cpu().numpy(), want)
+
+
 def test_decode_graph_replay(cuda, decode_b8):
     import torch
     from sparse_indexer import indexer_decode_pool_topk
