@@ -312,21 +312,32 @@ __device__ Threshold radix_threshold(SelShared<kThreads>& sh, ForKeys for_keys, 
     if (pass == 1)   // pass 0's histogram is no longer read: clear it for pass 2
       for (int b = tid; b < kHistBins; b += kThreads) sh.hist[0][b] = 0u;
     __syncthreads();
-    // Thread tid owns bpt bins counted from the top: the keys in higher bins
-    // are the wave totals of lower waves plus the lanes below in this wave.
+    // Thread tid owns bpt bins counted from the top (held in registers): the
+    // keys in higher bins are the wave totals of lower waves plus the lanes
+    // below in this wave.
+    constexpr int kMaxBpt = kHistBins / kThreads;
     const int bpt = nb >= kThreads ? nb / kThreads : 1;
     const int b0 = nb - bpt * (tid + 1);
-    uint32_t mine = 0;
+    uint32_t hb[kMaxBpt];
+#pragma unroll
+    for (int i = 0; i < kMaxBpt; i++) hb[i] = 0u;
     if (b0 >= 0) {
       if ((bpt & 3) == 0) {
-        for (int b = b0; b < b0 + bpt; b += 4) {
-          const uint4 v = *reinterpret_cast<const uint4*>(hist + b);
-          mine += v.x + v.y + v.z + v.w;
-        }
+#pragma unroll
+        for (int q = 0; q < kMaxBpt / 4; q++)
+          if (4 * q < bpt) {
+            const uint4 v = *reinterpret_cast<const uint4*>(hist + b0 + 4 * q);
+            hb[4 * q] = v.x; hb[4 * q + 1] = v.y; hb[4 * q + 2] = v.z; hb[4 * q + 3] = v.w;
+          }
       } else {
-        for (int b = b0; b < b0 + bpt; b++) mine += hist[b];
+#pragma unroll
+        for (int i = 0; i < kMaxBpt; i++)
+          if (i < bpt) hb[i] = hist[b0 + i];
       }
     }
+    uint32_t mine = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxBpt; i++) mine += hb[i];
     const uint32_t incl = wave_incl_scan(mine);
     if (lane == 63) sh.wsum[w] = incl;
     __syncthreads();
@@ -335,15 +346,19 @@ __device__ Threshold radix_threshold(SelShared<kThreads>& sh, ForKeys for_keys, 
     for (int i = 0; i < kWaves; i++) excl += i < w ? sh.wsum[i] : 0u;
     if (b0 >= 0 && excl < need && excl + mine >= need) {
       uint32_t above = excl;
-      for (int b = b0 + bpt - 1; b >= b0; b--) {
-        const uint32_t h = hist[b];
-        if (above + h >= need) {
-          sh.pick[0] = static_cast<uint32_t>(b);
-          sh.pick[1] = above;
-          sh.pick[2] = h;
-          break;
+      bool found = false;
+#pragma unroll
+      for (int i = kMaxBpt - 1; i >= 0; i--) {
+        if (i < bpt && !found) {
+          if (above + hb[i] >= need) {
+            sh.pick[0] = static_cast<uint32_t>(b0 + i);
+            sh.pick[1] = above;
+            sh.pick[2] = hb[i];
+            found = true;
+          } else {
+            above += hb[i];
+          }
         }
-        above += h;
       }
     }
     __syncthreads();
