@@ -17,15 +17,16 @@
 // scale bytes].
 //
 // Logits kernel: workgroup = (token, run of keys); 4 wavefronts, each takes
-// 16 keys at a time.  Per 16 keys: the 16 keys' 128 bytes (one contiguous
+// a run of 16-key groups.  Per group: the 16 keys' 128 bytes (one contiguous
 // 2 KB block when the keys share a page) and scales, then 4 x (H/16)
 // v_mfma_f32_16x16x32_fp8_fp8 with A = q (16 heads x 32 dims), B = k^T
 // (32 dims x 16 keys).  Lane (g, c) of D holds key c for heads 4g + [0, 4)
 // of each head tile, so the relu-weighted head sum is 4 FMAs per tile and
 // two cross-row swaps.  Each lane's B operand is dims [32g, 32g + 32) of key
 // c (32 contiguous bytes) and the A operand the same dims of its head, so
-// k-slot 8g + e of MFMA m is dim 32g + 8m + e on both sides.  A wave issues
-// the loads of all its groups before the first MFMA.
+// k-slot 8g + e of MFMA m is dim 32g + 8m + e on both sides.  A wave reads
+// its groups' block-table entries at once and streams the groups through a
+// register ring with three groups' loads in flight.
 //
 // Top-k: order-preserving 32-bit keys, radix select with 12-, 12- and 8-bit
 // digits (LDS histograms) for the k-th largest key, then an ordered
@@ -64,7 +65,7 @@ struct LogitsArgs {
   int max_blocks;
   int num_heads;
   int max_len;              // logits columns
-  int keys_per_wg;
+  int keys_per_wg;          // 64 * groups per wave
   float* logits;            // [T][max_len], row stride sl_t
   int64_t sl_t;
   int clean;                // write -inf at positions >= context length
@@ -78,102 +79,138 @@ __device__ __forceinline__ float row_sum4(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int kGroups>
+// Loads of one 16-key group (keys j0 + c) into registers: the 32 key bytes
+// of this lane (dims 32g + [0, 32)) and the key's scale.  blk is the page of
+// the group's first key (uniform); keys of a group straddle pages only when
+// block_size % 16 != 0 (kAligned false), and then read their own table
+// entry -- a dependent load, which drains the loads in flight, so aligned
+// block sizes take the path without it.
+struct Group {
+  uint4 kd[2];
+  float sc;    // the key's scale (meaningful when kok)
+  bool live;   // the group's first page is in the cache (uniform)
+  bool kok;    // this lane's key is valid and its page in the cache
+};
+
+template <bool kAligned>
+__device__ __forceinline__ void load_group(const LogitsArgs& a, int t, int j0, int blk, int len, int g, int c,
+                                           Group& gr) {
+  const int j = j0 + c;
+  gr.live = blk >= 0 && blk < a.num_blocks;
+  const int jb = j < len ? j : j0;
+  int bj = blk;
+  if (!kAligned && gr.live && jb / a.block_size != j0 / a.block_size) bj = a.bt[t * a.bt_stride + jb / a.block_size];
+  const bool ok = gr.live && bj >= 0 && bj < a.num_blocks;
+  // The loads are issued on every path (page 0 stands in for a page outside
+  // the cache), so the count of loads in flight is the same on all paths
+  // and a wait for one group never drains the later groups' loads.
+  const uint8_t* page = a.kv + static_cast<int64_t>(ok ? bj : 0) * a.page_bytes;
+  const int off = jb % a.block_size;
+  const uint4* kp = reinterpret_cast<const uint4*>(page + static_cast<int64_t>(off) * kHeadDim + 32 * g);
+  gr.kd[0] = kp[0];
+  gr.kd[1] = kp[1];
+  gr.kok = ok && j < len;
+  gr.sc = *reinterpret_cast<const float*>(page + static_cast<int64_t>(a.block_size) * kHeadDim + 4 * off);
+}
+
+// Wave = a run of kN 16-key groups of one token's row; the block-table
+// entries of all its groups are read at once (lane i: group i), then the
+// groups stream through a kDepth-deep ring of register slots, the loads of
+// group i + kDepth - 1 issued before group i is reduced, so each wave keeps
+// kDepth - 1 groups (6 KB at depth 4) in flight.  The run is unrolled
+// whole and its loads issued on every path, and the results wait in LDS
+// for stores after the last load (stores count with the loads in vmcnt):
+// every wait then counts exactly the group it needs.
+template <int kTiles, int kN, bool kAligned>
 __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(const LogitsArgs a) {
+  constexpr int kDepth = 4;
   const int t = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   const int g = lane >> 4, c = lane & 15;
-  const int j_begin = blockIdx.x * a.keys_per_wg;
-  const int j_end = j_begin + a.keys_per_wg < a.max_len ? j_begin + a.keys_per_wg : a.max_len;
+  const int j_wave = blockIdx.x * a.keys_per_wg + w * 16 * kN;
+  const int j_end = j_wave + 16 * kN < a.max_len ? j_wave + 16 * kN : a.max_len;
+  if (j_wave >= j_end) return;   // uniform (no barriers in this kernel)
+  const int n = (j_end - j_wave + 15) / 16;
   const int cap = a.max_blocks * a.block_size;
   int len = a.ctx[t];
   len = len < 0 ? 0 : len > cap ? cap : len;
-  const int n_tiles = a.num_heads / 16;
 
-  // q fragments (A operand) and the weights of this lane's heads.
-  uint64_t qf[kMaxHeads / 16][4];
-  float wv[kMaxHeads / 16][4];
-#pragma unroll
-  for (int ht = 0; ht < kMaxHeads / 16; ht++) {
-    if (ht < n_tiles) {
-      const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (16 * ht + c) * a.sq_h + 32 * g);
-      const uint4 lo = qp[0], hi = qp[1];
-      qf[ht][0] = (static_cast<uint64_t>(lo.y) << 32) | lo.x;
-      qf[ht][1] = (static_cast<uint64_t>(lo.w) << 32) | lo.z;
-      qf[ht][2] = (static_cast<uint64_t>(hi.y) << 32) | hi.x;
-      qf[ht][3] = (static_cast<uint64_t>(hi.w) << 32) | hi.z;
-#pragma unroll
-      for (int i = 0; i < 4; i++) wv[ht][i] = a.w[t * a.sw_t + 16 * ht + 4 * g + i];
-    } else {
-#pragma unroll
-      for (int m = 0; m < 4; m++) qf[ht][m] = 0;
-#pragma unroll
-      for (int i = 0; i < 4; i++) wv[ht][i] = 0.f;
-    }
+  // page of each group's first key (lane i < n: group i; -1 past the context)
+  int blk_l = -1;
+  if (lane < n) {
+    const int j0 = j_wave + 16 * lane;
+    if (j0 < len) blk_l = a.bt[t * a.bt_stride + j0 / a.block_size];
   }
 
-  const int64_t key_bytes = static_cast<int64_t>(a.block_size) * kHeadDim;
+  // q fragments (A operand) and the weights of this lane's heads.
+  uint64_t qf[kTiles][4];
+  float wv[kTiles][4];
+#pragma unroll
+  for (int ht = 0; ht < kTiles; ht++) {
+    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (16 * ht + c) * a.sq_h + 32 * g);
+    const uint4 lo = qp[0], hi = qp[1];
+    qf[ht][0] = (static_cast<uint64_t>(lo.y) << 32) | lo.x;
+    qf[ht][1] = (static_cast<uint64_t>(lo.w) << 32) | lo.z;
+    qf[ht][2] = (static_cast<uint64_t>(hi.y) << 32) | hi.x;
+    qf[ht][3] = (static_cast<uint64_t>(hi.w) << 32) | hi.z;
+#pragma unroll
+    for (int i = 0; i < 4; i++) wv[ht][i] = a.w[t * a.sw_t + 16 * ht + 4 * g + i];
+  }
+
   float* out = a.logits + t * a.sl_t;
-  // This wave's groups: keys j0 = j_begin + 16 * (w + kLogitWaves * u).
-  for (int base = j_begin + 16 * w; base < j_end; base += 16 * kLogitWaves * kGroups) {
-    uint4 kd[kGroups][2];
-    float sc[kGroups];
-    bool live[kGroups];   // the group's first page is in the cache (uniform)
-    bool kok[kGroups];    // this lane's key is valid and its page in the cache
+  __shared__ float res[kLogitWaves][16 * kN];
+  __shared__ uint8_t put[kLogitWaves][16 * kN];   // 1: write res, 0: leave the position untouched
+  Group ring[kDepth];
+  // group i of the run, or past the run's end (a row's tail) its last group
+  // again, loaded and not used
+  auto load = [&](int i, Group& gr) {
+    const int ic = i < n ? i : n - 1;
+    load_group<kAligned>(a, t, j_wave + 16 * ic, __builtin_amdgcn_readlane(blk_l, ic), len, g, c, gr);
+  };
 #pragma unroll
-    for (int u = 0; u < kGroups; u++) {
-      const int j0 = base + 16 * kLogitWaves * u;
-      const int j = j0 + c;
-      int blk = -1;
-      if (j0 < j_end && j0 < len) blk = a.bt[t * a.bt_stride + j0 / a.block_size];   // uniform
-      live[u] = blk >= 0 && blk < a.num_blocks;
-      kd[u][0] = kd[u][1] = make_uint4(0, 0, 0, 0);
-      sc[u] = 0.f;
-      kok[u] = false;
-      if (live[u]) {
-        // keys of a 16-group may straddle a page only when block_size % 16 != 0
-        const int jb = j < len ? j : j0;
-        const int bj = jb / a.block_size == j0 / a.block_size ? blk : a.bt[t * a.bt_stride + jb / a.block_size];
-        const bool ok = bj >= 0 && bj < a.num_blocks;
-        const uint8_t* page = a.kv + static_cast<int64_t>(ok ? bj : 0) * a.page_bytes;
-        const int off = jb % a.block_size;
-        const uint4* kp = reinterpret_cast<const uint4*>(page + static_cast<int64_t>(off) * kHeadDim + 32 * g);
-        kd[u][0] = kp[0];
-        kd[u][1] = kp[1];
-        kok[u] = ok && j < len;
-        sc[u] = kok[u] ? *reinterpret_cast<const float*>(page + key_bytes + 4 * off) : 0.f;
-      }
-    }
+  for (int s = 0; s < kDepth - 1; s++)
+    if (s < kN) load(s, ring[s]);
+  {
 #pragma unroll
-    for (int u = 0; u < kGroups; u++) {
-      const int j0 = base + 16 * kLogitWaves * u;
-      if (j0 >= j_end) break;   // uniform
-      const int j = j0 + c;
+    for (int i = 0; i < kN; i++) {
+      if (i + kDepth - 1 < kN) load(i + kDepth - 1, ring[(i + kDepth - 1) % kDepth]);
+      if (i >= n) continue;   // uniform (the tail of a row)
+      const Group& gr = ring[i % kDepth];
+      const int j = j_wave + 16 * i + c;
       float v = 0.f;
-      if (live[u]) {
-        const uint64_t k0 = (static_cast<uint64_t>(kd[u][0].y) << 32) | kd[u][0].x;
-        const uint64_t k1 = (static_cast<uint64_t>(kd[u][0].w) << 32) | kd[u][0].z;
-        const uint64_t k2 = (static_cast<uint64_t>(kd[u][1].y) << 32) | kd[u][1].x;
-        const uint64_t k3 = (static_cast<uint64_t>(kd[u][1].w) << 32) | kd[u][1].z;
+      const float sc = gr.kok ? gr.sc : 0.f;
+      if (gr.live) {
+        const uint64_t k0 = (static_cast<uint64_t>(gr.kd[0].y) << 32) | gr.kd[0].x;
+        const uint64_t k1 = (static_cast<uint64_t>(gr.kd[0].w) << 32) | gr.kd[0].z;
+        const uint64_t k2 = (static_cast<uint64_t>(gr.kd[1].y) << 32) | gr.kd[1].x;
+        const uint64_t k3 = (static_cast<uint64_t>(gr.kd[1].w) << 32) | gr.kd[1].z;
 #pragma unroll
-        for (int ht = 0; ht < kMaxHeads / 16; ht++) {
-          if (ht >= n_tiles) break;   // uniform
+        for (int ht = 0; ht < kTiles; ht++) {
           f32x4v d = {0.f, 0.f, 0.f, 0.f};
           d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][0]), static_cast<long>(k0), d, 0, 0, 0);
           d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][1]), static_cast<long>(k1), d, 0, 0, 0);
           d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][2]), static_cast<long>(k2), d, 0, 0, 0);
           d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][3]), static_cast<long>(k3), d, 0, 0, 0);
 #pragma unroll
-          for (int i = 0; i < 4; i++) v = __builtin_fmaf(wv[ht][i], fmaxf(sc[u] * d[i], 0.f), v);
+          for (int e = 0; e < 4; e++) v = __builtin_fmaf(wv[ht][e], fmaxf(sc * d[e], 0.f), v);
         }
         v = row_sum4(v);
       }
-      if (g == 0 && j < j_end) {
-        if (kok[u]) out[j] = v;
-        else if (j < len || a.clean) out[j] = -__builtin_inff();   // page outside the cache, or past the context
+      if (g == 0) {
+        // page outside the cache, or past the context: -inf (past the context only when cleaning)
+        res[w][16 * i + c] = gr.kok ? v : -__builtin_inff();
+        put[w][16 * i + c] = j < j_end && (gr.kok || j < len || a.clean);
       }
     }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int r = 0; r < (16 * kN + 63) / 64; r++) {
+    const int idx = 64 * r + lane;
+    if (idx < 16 * n && put[w][idx]) out[j_wave + idx] = res[w][idx];
   }
 }
 
@@ -579,6 +616,39 @@ __global__ __launch_bounds__(kSweepThreads) void topk_sweep_kernel(const TopkArg
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
+template <int kTiles, bool kAligned>
+void (*pick_logits_n(int gpw))(LogitsArgs) {
+  switch (gpw) {
+    case 1: return fp8_paged_mqa_logits_kernel<kTiles, 1, kAligned>;
+    case 2: return fp8_paged_mqa_logits_kernel<kTiles, 2, kAligned>;
+    case 4: return fp8_paged_mqa_logits_kernel<kTiles, 4, kAligned>;
+    case 8: return fp8_paged_mqa_logits_kernel<kTiles, 8, kAligned>;
+    default: return fp8_paged_mqa_logits_kernel<kTiles, 16, kAligned>;
+  }
+}
+
+// Kernel for 16 * tiles heads and gpw groups per wave (unaligned block
+// sizes: one group per wave only).
+template <bool kAligned>
+void (*pick_logits_kernel(int tiles, int gpw))(LogitsArgs) {
+  if constexpr (kAligned) {
+    switch (tiles) {
+      case 1: return pick_logits_n<1, true>(gpw);
+      case 2: return pick_logits_n<2, true>(gpw);
+      case 3: return pick_logits_n<3, true>(gpw);
+      default: return pick_logits_n<4, true>(gpw);
+    }
+  } else {
+    (void)gpw;
+    switch (tiles) {
+      case 1: return fp8_paged_mqa_logits_kernel<1, 1, false>;
+      case 2: return fp8_paged_mqa_logits_kernel<2, 1, false>;
+      case 3: return fp8_paged_mqa_logits_kernel<3, 1, false>;
+      default: return fp8_paged_mqa_logits_kernel<4, 1, false>;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace glm53
 
@@ -601,23 +671,23 @@ extern "C" int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t s
       (block_size * kHeadDim) % 4 || !aligned(weights, 4) || !aligned(logits, 4))
     return GLM53_ERR_MISALIGNED;
   if (num_tokens == 0 || max_len == 0) return 0;
-  // 16 groups (1024 keys) per workgroup when that still gives the CUs a few
-  // workgroups each, else 4 (256 keys).
-  const int64_t wg_large = num_tokens * ((max_len + 1023) / 1024);
-  const bool large = wg_large >= 512;
-  const int keys_per_wg = large ? 16 * kLogitWaves * 16 : 16 * kLogitWaves * 4;
+  // Runs of 2^m groups per wave, sized for about 512 workgroups over all
+  // rows (one resident round at 2 workgroups per CU), 1 to 16 groups; one
+  // group when groups straddle pages (block_size % 16 != 0).
+  const bool al = block_size % 16 == 0;
+  const int64_t groups = num_tokens * ((max_len + 15) / 16);
+  int gpw = 1;
+  while (al && gpw < 16 && groups >= int64_t(kLogitWaves) * 512 * gpw * 2) gpw *= 2;
+  const int keys_per_wg = 16 * kLogitWaves * gpw;
   LogitsArgs a{static_cast<const uint8_t*>(q), sq_t, sq_h, static_cast<const uint8_t*>(kv_cache), page_bytes,
                static_cast<int>(block_size), static_cast<int>(num_blocks), weights, sw_t, context_lens,
                block_table, bt_stride, static_cast<int>(max_blocks), static_cast<int>(num_heads),
                static_cast<int>(max_len), keys_per_wg, logits, sl_t, clean_logits ? 1 : 0};
   const dim3 grid(static_cast<unsigned>((max_len + keys_per_wg - 1) / keys_per_wg), static_cast<unsigned>(num_tokens));
   (void)hipGetLastError();
-  if (large)
-    hipLaunchKernelGGL(fp8_paged_mqa_logits_kernel<16>, grid, dim3(kLogitThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
-  else
-    hipLaunchKernelGGL(fp8_paged_mqa_logits_kernel<4>, grid, dim3(kLogitThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
+  const int tiles = static_cast<int>(num_heads / 16);
+  void (*kernel)(LogitsArgs) = al ? pick_logits_kernel<true>(tiles, gpw) : pick_logits_kernel<false>(tiles, 1);
+  hipLaunchKernelGGL(kernel, grid, dim3(kLogitThreads), 0, static_cast<hipStream_t>(stream), a);
   return static_cast<int>(hipGetLastError());
 }
 
