@@ -16,7 +16,9 @@ in the reference's measurements; the cold figures flush it (a 1 GiB write)
 before every timed step.
 
 Extra fields: the B=1 decode, the 262144-row store_int8 writer, the MoE
-align (16 calls per graph, as docs/measurements.json:1445 records), the
+align (16 calls per graph, as docs/measurements.json:1445 records), the W4A16
+MoE layer (B=1..8), the sparse indexer's decode scoring (FP8 paged logits
+and top-512 pools over 65536 pools per request, B=1 and B=8), the
 prefill-shaped T=2048 call, and the CPU baseline (the C oracle on the host
 cores, a bounded sample of the same workload).
 
@@ -350,6 +352,46 @@ def main():
             del gw, gr, calls
         extra["moe_w4a16_layer"] = moew
         del layers
+
+        # ------------------------------------------------------------ sparse indexer (decode)
+        # FP8 paged MQA logits of each request's 65536 pools (262144-token
+        # context, 4 tokens per pool, 32 heads, 64-pool pages), then the
+        # top-512 pools per request.  "warm": one call replayed (its pool
+        # cache stays in the 256 MB MALL); "rotation" (the decode case, each
+        # layer reading its own cache): calls cycling over enough caches
+        # (> 512 MB) that every call reads its cache from HBM.
+        from sparse_indexer import fp8_paged_mqa_logits, indexer_topk, indexer_decode_pool_topk
+        idx = {}
+        for b, n_caches in ((1, 64), (8, 8)):
+            gi = W.gen(dev, W.SEED_BENCH + 200 + b)
+            sets = [W.indexer_decode_inputs(dev, gi, batch=b) for _ in range(n_caches)]
+            q_i, cache_i, w_i, lens_i, bt_i, pools = sets[0]
+            logits_i = fp8_paged_mqa_logits(q_i, cache_i, w_i, lens_i, bt_i, pools, clean_logits=False)
+            row = {}
+            log(f"indexer decode B={b}")
+            for name, fn in (("logits", lambda s: fp8_paged_mqa_logits(*s, clean_logits=False)),
+                             ("logits_plus_topk", lambda s: indexer_decode_pool_topk(*s))):
+                gg, _ = capture(torch, lambda: fn(sets[0]), args.unroll)
+                gr, _ = capture(torch, lambda: [fn(s) for s in sets], 1)
+                for _ in range(3):
+                    gg.replay()
+                    gr.replay()
+                row[f"us_{name}_warm"] = round(timer.replay_loop(gg, max(2, K // args.unroll // 2)) / args.unroll, 2)
+                row[f"us_{name}_rotation"] = round(timer.replay_loop(gr, 10) / n_caches, 2)
+                del gg, gr
+            gt, _ = capture(torch, lambda: indexer_topk(logits_i, lens_i, W.INDEX_TOPK_POOLS), args.unroll)
+            gt.replay()
+            row["us_topk"] = round(timer.replay_loop(gt, max(2, K // args.unroll // 2)) / args.unroll, 2)
+            del gt
+            nb = W.indexer_bytes(lens_i)
+            row["logits_algorithmic_bytes"] = nb
+            for tag in ("warm", "rotation"):
+                gbs = nb / (row[f"us_logits_{tag}"] * 1e-6) / 1e9
+                row[f"logits_gbs_{tag}"] = round(gbs, 1)
+                row[f"logits_hbm_frac_{tag}"] = round(gbs / HBM_PEAK_GBS, 3)
+            idx[f"B{b}"] = row
+            del sets, q_i, cache_i, w_i, lens_i, bt_i, logits_i
+        extra["indexer_decode"] = idx
 
         # ------------------------------------------------------------ prefill-shaped
         qp, idxp, new_rows, pslots = W.prefill_inputs(dev, g8)
