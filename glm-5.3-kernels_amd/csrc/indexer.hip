@@ -234,6 +234,7 @@ struct TopkArgs {
   int32_t* cand_pos;        // [rows][chunks * k] their positions
   int chunks;
   int chunk_len;
+  bool vec;                 // logits rows 16-byte aligned
 };
 
 // Order-preserving key: a larger float has a larger key; NaN -> 0, below
@@ -442,14 +443,15 @@ __device__ void emit_selected(SelShared<kThreads>& sh, const uint32_t (&kk)[P], 
   }
 }
 
-// Keys of row positions i0 + [0, P) (P a multiple of 4, i0 a multiple of 4,
-// x 16-byte aligned); positions at or past n get key 0.
+// Keys of row positions i0 + [0, P) (P and i0 multiples of 4); positions at
+// or past n get key 0.  vec: x is 16-byte aligned (rows of a stride that is
+// a multiple of 4 floats), else every key is its own load.
 template <int P>
-__device__ __forceinline__ void load_row_keys(const float* x, int n, int i0, uint32_t (&kk)[P]) {
+__device__ __forceinline__ void load_row_keys(const float* x, int n, int i0, bool vec, uint32_t (&kk)[P]) {
 #pragma unroll
   for (int q = 0; q < P / 4; q++) {
     const int p = i0 + 4 * q;
-    if (p + 3 < n) {
+    if (vec && p + 3 < n) {
       const float4 v = *reinterpret_cast<const float4*>(x + p);
       kk[4 * q] = order_key(v.x); kk[4 * q + 1] = order_key(v.y);
       kk[4 * q + 2] = order_key(v.z); kk[4 * q + 3] = order_key(v.w);
@@ -486,7 +488,7 @@ __global__ __launch_bounds__(kChunkThreads) void topk_chunk_kernel(const TopkArg
   const int valid = rest < 0 ? 0 : rest > a.chunk_len ? a.chunk_len : rest;
   if (len <= k || valid == 0) return;   // uniform
   uint32_t kk[P];
-  load_row_keys<P>(a.logits + row * a.sl + start, valid, tid * P, kk);
+  load_row_keys<P>(a.logits + row * a.sl + start, valid, tid * P, a.vec, kk);
   const int64_t cb = (static_cast<int64_t>(row) * a.chunks + c) * k;
   uint32_t* ck = a.cand_key + cb;
   int32_t* cp = a.cand_pos + cb;
@@ -565,7 +567,7 @@ __global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(const TopkArg
       if (++sl == k) { sl = 0; c++; }
     }
   } else {
-    load_row_keys<P>(a.logits + row * a.sl, len, tid * P, kk);
+    load_row_keys<P>(a.logits + row * a.sl, len, tid * P, a.vec, kk);
 #pragma unroll
     for (int j = 0; j < P; j++)
       if (tid * P + j < len) { kmin = min(kmin, kk[j]); kmax = max(kmax, kk[j]); }
@@ -595,7 +597,7 @@ __global__ __launch_bounds__(kSweepThreads) void topk_sweep_kernel(const TopkArg
   const Threshold t = radix_threshold(sh, [&](auto f) {
     for (int sw = 0; sw < sweeps; sw++) {
       uint32_t kk[kSweepKeys];
-      load_row_keys<kSweepKeys>(x + sw * kSweep, len - sw * kSweep, tid * kSweepKeys, kk);
+      load_row_keys<kSweepKeys>(x + sw * kSweep, len - sw * kSweep, tid * kSweepKeys, a.vec, kk);
       for_each_key(kk, f);
     }
   }, static_cast<uint32_t>(k), 0u, ~0u);
@@ -603,7 +605,7 @@ __global__ __launch_bounds__(kSweepThreads) void topk_sweep_kernel(const TopkArg
   for (int sw = 0; sw < sweeps; sw++) {
     uint32_t kk[kSweepKeys];
     const int base = sw * kSweep;
-    load_row_keys<kSweepKeys>(x + base, len - base, tid * kSweepKeys, kk);
+    load_row_keys<kSweepKeys>(x + base, len - base, tid * kSweepKeys, a.vec, kk);
     uint32_t n_eq, n_sel;
     emit_selected(sh, kk, t, eq_seen, written, [&](uint32_t o, int j) {
       if (o < static_cast<uint32_t>(k)) out[o] = base + tid * kSweepKeys + j;
@@ -760,12 +762,12 @@ extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t
   if (!logits || !lengths || !out) return GLM53_ERR_NULL_POINTER;
   if (!topk_shape_ok(num_rows, max_len, k) || sl < max_len || so < k) return GLM53_ERR_BAD_SHAPE;
   if (num_rows == 0) return 0;
-  if (!aligned(logits, 16) || sl % 4) return GLM53_ERR_MISALIGNED;
+  if (!aligned(logits, 4)) return GLM53_ERR_MISALIGNED;
   const TopkPlan plan = plan_topk(max_len, k);
   const int64_t need = topk_ws_bytes(plan, num_rows, k);
   if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 16))) return GLM53_ERR_WORKSPACE;
   TopkArgs a{logits, sl, lengths, static_cast<int>(max_len), static_cast<int>(k), out, so, nullptr, nullptr,
-             plan.chunks, plan.chunk_len};
+             plan.chunks, plan.chunk_len, aligned(logits, 16) && sl % 4 == 0};
   if (need) {
     a.cand_key = static_cast<uint32_t*>(workspace);
     a.cand_pos = reinterpret_cast<int32_t*>(a.cand_key + num_rows * plan.chunks * k);

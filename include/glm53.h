@@ -329,7 +329,8 @@ int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t sq_h,
  * largest of logits[r, 0 : lengths[r]] (lengths clamped to [0, max_len]; NaN
  * ranks lowest, ties by smaller position), written as positions in ascending
  * order; a row with fewer than k valid positions gets all of them, then -1.
- *   logits     fp32 [num_rows][max_len], row stride sl (16-byte aligned, sl % 4 == 0)
+ *   logits     fp32 [num_rows][max_len], row stride sl (rows 16-byte aligned load
+ *              4 keys at a time, others one at a time)
  *   workspace  device scratch of glm53_indexer_topk_workspace_bytes(...) bytes
  *              (0 for rows of at most 4096 columns; may then be NULL)
  *   out        int32 [num_rows][k], row stride so

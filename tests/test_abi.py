@@ -296,7 +296,7 @@ def test_indexer_host_errors():
     assert bad(5, 0) == -2
     assert bad(5, 2048) == -2       # k above the row length
     assert bad(9, 100) == -2        # output row stride below k
-    assert bad(1, 1026) == -3       # row stride not a multiple of 4 floats
+    assert bad(0, ctypes.c_void_p(0x10002)) == -3   # logits not float-aligned
     assert bad(3, 0) == 0
     # long rows run in two stages and need the candidates' workspace
     ws = L.glm53_indexer_topk_workspace_bytes

@@ -175,6 +175,22 @@ def test_topk_every_plan(cuda, oracle, n, k):
     assert np.array_equal(got.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("n,k", [(4095, 512), (70001, 512)])
+def test_topk_unaligned_rows(cuda, oracle, n, k):
+    """Row strides that are not a multiple of 4 floats (pool counts of any
+    size): keys load one at a time; one workgroup per row and the two stages."""
+    import torch
+    from sparse_indexer import indexer_topk
+    g = torch.Generator(device=cuda).manual_seed(n)
+    x = torch.randn(3, n, generator=g, device=cuda)
+    x[1] = torch.randint(0, 5, (n,), generator=g, device=cuda).float()
+    lens = torch.tensor([n, n - 7, k + 3], dtype=torch.int32, device=cuda)
+    log_case("indexer top-k unaligned rows", n, k)
+    got = indexer_topk(x, lens, k)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), oracle.indexer_topk(x.cpu().numpy(), lens.cpu().numpy(), k))
+
+
 def test_decode_graph_replay(cuda, decode_b8):
     import torch
     from sparse_indexer import indexer_decode_pool_topk
