@@ -437,6 +437,43 @@ def main():
                              "median of 5 runs of the C oracle",
                    "us_per_step": round(us_cpu, 1), "us_per_step_1thread": round(us_cpu1, 1)}
 
+            # The widened rows' CPU paths (the numpy oracle: float64 reference
+            # arithmetic, one call each) beside their GPU figures above.
+            rows_cpu = {}
+            lay = W.moe_w4a16_layer(dev, seed=W.SEED_BENCH + 100)
+            bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+            w13n, s13n = lay["w13_packed"].cpu().numpy(), bits(lay["w13_scale"])
+            w2n, s2n = lay["w2_packed"].cpu().numpy(), bits(lay["w2_scale"])
+            del lay
+            for b in (1, 8):
+                xm, idm, twm = W.moe_w4a16_inputs(b, dev, W.gen(dev, W.SEED_BENCH + b))
+                log(f"CPU oracle: W4A16 MoE layer B={b}")
+                t0 = time.perf_counter()
+                oracle.moe_w4a16(bits(xm), w13n, s13n, w2n, s2n, twm.cpu().numpy(), idm.cpu().numpy())
+                us_c = (time.perf_counter() - t0) * 1e6
+                gpu_us = extra["moe_w4a16_layer"][f"B{b}"]["us_per_call_layer_rotation"]
+                rows_cpu[f"moe_w4a16_layer_B{b}"] = {"cpu_us": round(us_c), "gpu_us": gpu_us,
+                                                     "speedup": round(us_c / gpu_us)}
+            del w13n, s13n, w2n, s2n
+            gi = W.gen(dev, W.SEED_BENCH + 201)
+            q_i, cache_i, w_i, lens_i, bt_i, pools = W.indexer_decode_inputs(dev, gi, batch=1)
+            page = cache_i.stride(0)
+            pages = torch.as_strided(cache_i, (cache_i.shape[0], page), (page, 1)).cpu().numpy()
+            log("CPU oracle: indexer logits + top-512 B=1")
+            t0 = time.perf_counter()
+            lg = oracle.fp8_paged_mqa_logits(q_i.view(torch.uint8).cpu().numpy().reshape(1, -1, 128), pages,
+                                             cache_i.shape[1], w_i.cpu().numpy(), lens_i.cpu().numpy(),
+                                             bt_i.cpu().numpy(), pools, clean=False)
+            oracle.indexer_topk(lg, lens_i.cpu().numpy(), W.INDEX_TOPK_POOLS)
+            us_c = (time.perf_counter() - t0) * 1e6
+            gpu_us = extra["indexer_decode"]["B1"]["us_logits_plus_topk_rotation"]
+            rows_cpu["indexer_logits_plus_topk_B1"] = {"cpu_us": round(us_c), "gpu_us": gpu_us,
+                                                       "speedup": round(us_c / gpu_us)}
+            del pages, lg, q_i, cache_i
+            rows_cpu["note"] = ("numpy oracle (float64 arithmetic, library threads as configured), one call; "
+                                "GPU figures: layer rotation / cache rotation")
+            extra["cpu_oracle_rows"] = rows_cpu
+
     # dominant kernel: sparse_mla_kernel (split attention); algorithmic bytes of
     # the step over its event-timed average duration.  traffic: measured HBM-side
     # bytes per dispatch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated).
