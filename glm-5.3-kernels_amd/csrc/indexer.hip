@@ -665,7 +665,8 @@ extern "C" int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t s
                                           void* stream) {
   if (!q || !kv_cache || !weights || !context_lens || !block_table || !logits) return GLM53_ERR_NULL_POINTER;
   if (head_dim != kHeadDim || num_heads < 16 || num_heads > kMaxHeads || num_heads % 16 || num_tokens < 0 ||
-      num_tokens > 65535 || block_size < 1 || num_blocks < 1 || max_blocks < 1 || max_len < 0 ||
+      num_tokens > 65535 || block_size < 1 || num_blocks < 1 || num_blocks > (int64_t(1) << 31) - 1 ||
+      max_blocks < 1 || max_len < 0 || max_len > (int64_t(1) << 30) ||
       max_blocks * block_size > (int64_t(1) << 31) - 1 || page_bytes < block_size * (kHeadDim + 4) ||
       sq_h < kHeadDim || sq_t < num_heads * sq_h || sw_t < num_heads || sl_t < max_len || bt_stride < max_blocks)
     return GLM53_ERR_BAD_SHAPE;

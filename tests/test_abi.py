@@ -286,6 +286,8 @@ def test_indexer_host_errors():
     assert bad(14, 80) == -2        # at most 64 heads
     assert bad(4, 64 * 132 - 16) == -2   # page smaller than block_size x 132
     assert bad(19, 1000) == -2      # logits row stride below max_len
+    assert bad(16, (1 << 30) + 1) == -2   # positions past 2^30
+    assert bad(6, 1 << 31) == -2    # block ids past int32
     assert bad(0, mis) == -3
     assert bad(4, 64 * 132 + 8) == -3    # page stride not a multiple of 16
     assert bad(13, 0) == 0          # nothing to do
