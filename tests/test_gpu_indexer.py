@@ -191,6 +191,32 @@ def test_topk_unaligned_rows(cuda, oracle, n, k):
     assert np.array_equal(got.cpu().numpy(), oracle.indexer_topk(x.cpu().numpy(), lens.cpu().numpy(), k))
 
 
+def test_decode_pool_topk_mtp_and_table_capacity(cuda, oracle):
+    """The fused decode call with next_n = 2 (each query row its own causal
+    length) and a context longer than its block table holds (the positions
+    the table cannot hold are neither scored nor selected)."""
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits, indexer_decode_pool_topk
+    g = torch.Generator(device=cuda).manual_seed(21)
+    bs, per_req = 64, 40
+    cache, nb = W.indexer_cache(cuda, g, 3 * per_req * bs, bs)
+    bt = torch.randperm(nb, generator=g, device=cuda).to(torch.int32)[: 3 * per_req].view(3, per_req).contiguous()
+    q = (torch.randn(3, 2, 32, 128, generator=g, device=cuda) * 60).to(torch.float8_e4m3fn)
+    w = torch.randn(6, 32, generator=g, device=cuda) / 32 ** 0.5
+    ctx = torch.tensor([per_req * bs, 700, per_req * bs + 500], dtype=torch.int32, device=cuda)
+    max_pools = per_req * bs + 512
+    log_case("indexer decode pool top-k, next_n 2, context past the table")
+    got = indexer_decode_pool_topk(q, cache, w, ctx, bt, max_pools)
+    logits = fp8_paged_mqa_logits(q, cache, w, ctx, bt, max_pools, clean_logits=False)
+    torch.cuda.synchronize()
+    rows_ctx = np.array([per_req * bs - 1, per_req * bs, 699, 700, per_req * bs, per_req * bs])   # clamped to the table
+    want = oracle.indexer_topk(logits.cpu().numpy(), rows_ctx, 512)
+    assert np.array_equal(got.cpu().numpy(), want)
+    # the logits of those rows against the float64 oracle (scored positions only)
+    check_logits(oracle, logits, q.view(6, 1, 32, 128), cache, w, torch.from_numpy(rows_ctx),
+                 bt.repeat_interleave(2, 0), max_pools, False)
+
+
 def test_decode_graph_replay(cuda, decode_b8):
     import torch
     from sparse_indexer import indexer_decode_pool_topk
