@@ -2,8 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 CPU-baseline leg of bench.py, always as the checker.  The product modules
-(titan_kv, titan_mla, titan_moe_align, titan_moe_w4a16, sparse_utils) never
-import it.
+(titan_kv, titan_mla, titan_moe_align, titan_moe_w4a16, sparse_utils,
+sparse_indexer) never import it.
 
 The arithmetic lives in glm53_oracle.c (built by oracle/Makefile into
 liboracle.so); this module wraps it for numpy arrays and restates the two
@@ -43,6 +43,18 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
   formulation (tests/test_oracle_moe_w4a16.py).  The clamp's exact form
   (gate clamped above, up clamped both ways, limit 10) is vLLM's and is not
   in the reference: parity of that detail with vLLM is unpinned.
+* e4m3_to_f32 / fp8_paged_mqa_logits, the indexer's decode scoring (vLLM's
+  fp8_paged_mqa_logits_triton, called at integration/patch_decode_indexer.py:
+  34-44, computing DeepGEMM's published definition): torch's float8_e4m3fn
+  decoding of all 256 codes, the closed form of a unit query, paging
+  invariance and masking, and an independent torch formulation
+  (tests/test_oracle_indexer.py).  Parity with vLLM's kernel itself is
+  unpinned (not in the container).
+* order_key / indexer_topk, the top-k per row whose output is pool_topk
+  (consumed at integration/patch_indexer_sharding.py:58-79): brute-force
+  selection on normal, tied, short and special-value rows
+  (tests/test_oracle_indexer.py).  The order inside ties (smaller position
+  first, NaN below -inf) is this build's definition.
 """
 from __future__ import annotations
 
