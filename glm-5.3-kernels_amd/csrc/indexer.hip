@@ -22,9 +22,12 @@
 // v_mfma_f32_16x16x32_fp8_fp8 with A = q (16 heads x 32 dims), B = k^T
 // (32 dims x 16 keys).  Lane (g, c) of D holds key c for heads 4g + [0, 4)
 // of each head tile, so the relu-weighted head sum is 4 FMAs per tile and
-// two cross-row swaps.  Each lane's B operand is dims [32g, 32g + 32) of key
-// c (32 contiguous bytes) and the A operand the same dims of its head, so
-// k-slot 8g + e of MFMA m is dim 32g + 8m + e on both sides.  A wave reads
+// two cross-row swaps.  Each lane's B operand is dims [16g, 16g + 16) and
+// [64 + 16g, 64 + 16g + 16) of key c and the A operand the same dims of its
+// head: k-slot 8g + e of MFMA m is dim 16g + 8m + e (m < 2), 64 + 16g +
+// 8(m - 2) + e (m >= 2) on both sides, so each of the two 16-byte load
+// instructions covers whole 64-byte halves of its 16 keys' lines (each half
+// requested once, however soon the L1 evicts it).  A wave reads
 // its groups' block-table entries at once and streams the groups through a
 // register ring with three groups' loads in flight.
 //
@@ -106,9 +109,9 @@ __device__ __forceinline__ void load_group(const LogitsArgs& a, int t, int j0, i
   // and a wait for one group never drains the later groups' loads.
   const uint8_t* page = a.kv + static_cast<int64_t>(ok ? bj : 0) * a.page_bytes;
   const int off = jb % a.block_size;
-  const uint4* kp = reinterpret_cast<const uint4*>(page + static_cast<int64_t>(off) * kHeadDim + 32 * g);
-  gr.kd[0] = kp[0];
-  gr.kd[1] = kp[1];
+  const uint4* kp = reinterpret_cast<const uint4*>(page + static_cast<int64_t>(off) * kHeadDim + 16 * g);
+  gr.kd[0] = kp[0];   // dims 16g + [0, 16): with the other 3 lane groups, the key's first 64-byte half
+  gr.kd[1] = kp[4];   // dims 64 + 16g + [0, 16): its second half
   gr.kok = ok && j < len;
   gr.sc = *reinterpret_cast<const float*>(page + static_cast<int64_t>(a.block_size) * kHeadDim + 4 * off);
 }
@@ -148,8 +151,8 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
   float wv[kTiles][4];
 #pragma unroll
   for (int ht = 0; ht < kTiles; ht++) {
-    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (16 * ht + c) * a.sq_h + 32 * g);
-    const uint4 lo = qp[0], hi = qp[1];
+    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (16 * ht + c) * a.sq_h + 16 * g);
+    const uint4 lo = qp[0], hi = qp[4];
     qf[ht][0] = (static_cast<uint64_t>(lo.y) << 32) | lo.x;
     qf[ht][1] = (static_cast<uint64_t>(lo.w) << 32) | lo.z;
     qf[ht][2] = (static_cast<uint64_t>(hi.y) << 32) | hi.x;
