@@ -17,7 +17,9 @@
 //     online softmax; the two are merged through LDS at the end.  Two waves
 //     per SIMD interleave their tiles, hiding each other's latencies.
 //   * Lane (g = lane / 16, c = lane % 16) gathers 32 bytes of its wave's
-//     slice from keys c and 16 + c of a tile: four 16-byte loads per tile.
+//     slice from keys c and 16 + c of a tile: four 16-byte loads per tile,
+//     slice bytes 16g + [0, 16) and 64 + 16g + [0, 16), so each load
+//     instruction covers whole 64-byte halves of the slice.
 //     The gathers of a whole chunk (8 tiles, 256 keys) are issued before any
 //     is consumed, so a decode split pays one index and one row latency.
 //   * S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = 16 keys x 32 latents
@@ -246,16 +248,17 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   const int32_t* pools_t = kMode == kPooledPos ? a.pools + t * a.sp_t : nullptr;
   const int seq_len_t = kMode == kPooledPos && a.seq_lens ? a.seq_lens[t] : -1;
 
-  // Q^T fragment (B operand of S^T = K Q^T): head c, latents
-  // [128 sl + 32g, +32) -> four K-steps of 8.
+  // Q^T fragment (B operand of S^T = K Q^T): head c, latents 128 sl + 16g +
+  // [0, 16) and 128 sl + 64 + 16g + [0, 16) -> four K-steps of 8 (the same
+  // latents as the lane's gathered key bytes).
   bf16x8 qf[4];
   {
     uint4 z = make_uint4(0, 0, 0, 0);
     uint4 q0 = z, q1 = z, q2 = z, q3 = z;
     if (head_ok) {
       const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + head * a.sq_h +
-                                                       kSlice * sl + 32 * g);
-      q0 = qp[0]; q1 = qp[1]; q2 = qp[2]; q3 = qp[3];
+                                                       kSlice * sl + 16 * g);
+      q0 = qp[0]; q1 = qp[1]; q2 = qp[8]; q3 = qp[9];
     }
     qf[0] = __builtin_bit_cast(bf16x8, q0);
     qf[1] = __builtin_bit_cast(bf16x8, q1);
@@ -308,9 +311,9 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         kd[r][u][1] = make_uint4(0, 0, 0, 0);
         if (kid >= 0) {
           const uint4* rp = reinterpret_cast<const uint4*>(
-              a.kv + static_cast<int64_t>(kid) * (kPaged ? 16 : a.skv) + kSlice * sl + 32 * g);
-          kd[r][u][0] = rp[0];
-          kd[r][u][1] = rp[1];
+              a.kv + static_cast<int64_t>(kid) * (kPaged ? 16 : a.skv) + kSlice * sl + 16 * g);
+          kd[r][u][0] = rp[0];   // slice bytes 16g + [0, 16): with the 3 other lane groups, its first 64 bytes
+          kd[r][u][1] = rp[4];   // slice bytes 64 + 16g + [0, 16): its last 64
         }
       }
       sv[r] = 0.f;
@@ -364,12 +367,12 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
           sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k45, qf[2], sacc, 0, 0, 0);
           sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k67, qf[3], sacc, 0, 0, 0);
           s_part[u] = sacc;
-          // V slice for the PV product: row 16u + c, latents [32g, +32) of the slice.
+          // V slice for the PV product: row 16u + c, latents 16g + [0, 16) and 64 + 16g + [0, 16).
           const int vrow = 16 * u + c;
-          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g)) = __builtin_bit_cast(uint4, k01);
-          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g + 8)) = __builtin_bit_cast(uint4, k23);
-          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g + 16)) = __builtin_bit_cast(uint4, k45);
-          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 32 * g + 24)) = __builtin_bit_cast(uint4, k67);
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 16 * g)) = __builtin_bit_cast(uint4, k01);
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 16 * g + 8)) = __builtin_bit_cast(uint4, k23);
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 64 + 16 * g)) = __builtin_bit_cast(uint4, k45);
+          *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 64 + 16 * g + 8)) = __builtin_bit_cast(uint4, k67);
         }
         sh.red[buf][kg][sl][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
         sh.red[buf][kg][sl][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
