@@ -452,10 +452,16 @@ def fp8_paged_mqa_logits(q_u8: np.ndarray, pages: np.ndarray, block_size: int, w
         q = table[q_u8[t]]                                                             # [H, D]
         w = np.asarray(weights[t], dtype=np.float64)
         dots = k @ q.T                                                                 # [n, H]
-        val = (np.maximum(s[:, None] * dots, 0.0) * w[None, :]).sum(axis=1)
+        # relu as fmax: a (key, head) product that is NaN (an E4M3 NaN code in
+        # k or q) contributes 0, as the kernels' fmaxf(x, 0) gives
+        val = (np.fmax(s[:, None] * dots, 0.0) * w[None, :]).sum(axis=1)
         out[t, :n] = np.where(ok, val, -np.inf)
         if bound:
-            mag[t, :n] = np.where(ok, (np.abs(s)[:, None] * (np.abs(k) @ np.abs(q).T) * np.abs(w)[None, :]).sum(axis=1), 0.0)
+            kk = np.nan_to_num(np.abs(k), nan=0.0)
+            qq = np.nan_to_num(np.abs(q), nan=0.0)
+            terms = np.abs(s)[:, None] * (kk @ qq.T) * np.abs(w)[None, :]
+            terms = np.where(np.isnan(s[:, None] * dots), 0.0, terms)                 # dropped terms: exactly 0
+            mag[t, :n] = np.where(ok, terms.sum(axis=1), 0.0)
     return (out, mag) if bound else out
 
 

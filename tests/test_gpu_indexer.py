@@ -217,6 +217,38 @@ def test_decode_pool_topk_mtp_and_table_capacity(cuda, oracle):
                  bt.repeat_interleave(2, 0), max_pools, False)
 
 
+def test_logits_nan_codes(cuda, oracle):
+    """E4M3 NaN codes in keys and in one head's query: the NaN products are
+    dropped by the relu (fmax), as the oracle defines."""
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits, indexer_topk
+    g = torch.Generator(device=cuda).manual_seed(31)
+    bs = 64
+    cache, nb = W.indexer_cache(cuda, g, 2 * 1024, bs)
+    bt = torch.arange(nb, device=cuda, dtype=torch.int32).view(2, -1).contiguous()
+    pages = torch.as_strided(cache, (nb, cache.stride(0)), (cache.stride(0), 1))   # page bytes
+    pages[0, 5 * 128 + 17] = 0x7F      # key 5 of row 0 (page 0), dim 17
+    pages[3, 0] = 0xFF                 # key 192 of row 0, dim 0
+    pages[nb - 1, 63 * 128 + 127] = 0x7F                                   # the last key of row 1, dim 127
+    pages[nb - 1, 64 * 128 + 4 * 62: 64 * 128 + 4 * 63] = torch.tensor(    # key 1022 of row 1: NaN scale
+        [0x00, 0x00, 0xC0, 0x7F], dtype=torch.uint8, device=cuda)
+    qf = torch.randn(2, 1, 32, 128, generator=g, device=cuda)
+    q = (qf * (448.0 / qf.abs().amax(dim=-1, keepdim=True))).to(torch.float8_e4m3fn)
+    q.view(torch.uint8)[1, 0, 9, 40] = 0x7F   # head 9 of row 1
+    w = torch.randn(2, 32, generator=g, device=cuda) / 32 ** 0.5
+    lens = torch.tensor([1024, 1024], dtype=torch.int32, device=cuda)
+    log_case("indexer logits with NaN codes")
+    got = fp8_paged_mqa_logits(q, cache, w, lens, bt, 1024)
+    torch.cuda.synchronize()
+    check_logits(oracle, got, q, cache, w, lens, bt, 1024, True)
+    g0 = got.cpu()
+    assert g0[0, 5] == 0 and g0[0, 192] == 0 and g0[1, 1022] == 0 and g0[1, 1023] == 0
+    assert torch.isfinite(g0).all()
+    top = indexer_topk(got, lens, 512)
+    torch.cuda.synchronize()
+    assert np.array_equal(top.cpu().numpy(), oracle.indexer_topk(g0.numpy(), lens.cpu().numpy(), 512))
+
+
 def test_decode_graph_replay(cuda, decode_b8):
     import torch
     from sparse_indexer import indexer_decode_pool_topk

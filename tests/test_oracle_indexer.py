@@ -145,3 +145,28 @@ def test_topk_brute_force(oracle):
         want = brute_topk(logits[r], lens[r], k)
         assert got[r, :len(want)].tolist() == want
         assert np.all(got[r, len(want):] == -1)
+
+
+def test_nan_products_are_dropped(oracle):
+    """relu is fmax: an E4M3 NaN code in a key or in one head's query makes
+    that (key, head) product NaN, which contributes 0."""
+    rng = np.random.default_rng(5)
+    n, H, bs = 64, 16, 16
+    keys = rng.integers(0, 256, size=(n, D), dtype=np.uint8)
+    keys[(keys & 0x7F) == 0x7F] = 0
+    keys[3, 10] = 0x7F                 # NaN code in key 3
+    scales = rng.uniform(0.1, 1.0, size=n).astype(np.float32)
+    q = rng.integers(0, 256, size=(1, H, D), dtype=np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0
+    w = rng.standard_normal((1, H)).astype(np.float32)
+    pages = page_layout(keys, scales, bs)
+    bt = np.arange(pages.shape[0], dtype=np.int32)[None, :]
+    base = oracle.fp8_paged_mqa_logits(q, pages, bs, w, np.array([n]), bt, n)
+    assert np.isfinite(base[0]).all() and base[0, 3] == 0.0     # every head's product with key 3 dropped
+    q2 = q.copy()
+    q2[0, 5, 7] = 0xFF                 # NaN code in head 5
+    got = oracle.fp8_paged_mqa_logits(q2, pages, bs, w, np.array([n]), bt, n)
+    w5 = w.copy()
+    w5[0, 5] = 0.0                     # head 5 removed instead
+    want = oracle.fp8_paged_mqa_logits(q, pages, bs, w5, np.array([n]), bt, n)
+    assert np.array_equal(got, want)
