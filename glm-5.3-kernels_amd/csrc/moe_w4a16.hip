@@ -234,8 +234,12 @@ __device__ __forceinline__ void finish_tile(GateUpShared& sh, int buf, const Gat
         g += rg[ww * 2 * 64 * 4];
         up += ru[ww * 2 * 64 * 4];
       }
-      g = fminf(bf16_round(g), a.clamp);
-      up = fminf(fmaxf(bf16_round(up), -a.clamp), a.clamp);
+      // compare-and-select rather than fminf/fmaxf: a NaN stays NaN (as
+      // torch.clamp keeps it) instead of becoming a limit
+      g = bf16_round(g);
+      up = bf16_round(up);
+      g = g > a.clamp ? a.clamp : g;
+      up = up > a.clamp ? a.clamp : up < -a.clamp ? -a.clamp : up;
       const float v = g / (1.0f + expf(-g)) * up;
       a.act[static_cast<int64_t>(route) * a.n_inter + kTileN * jt + n] = static_cast<uint16_t>(f32_to_bf16_bits(v));
     }

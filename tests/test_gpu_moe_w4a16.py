@@ -173,6 +173,26 @@ def test_clamp_off_row_stride_and_output(cuda, oracle, moe):
     assert not torch.equal(out, clamped)          # 3-sigma inputs push gate/up past 10
 
 
+def test_nan_token_propagates(cuda, oracle, moe):
+    """A NaN in one token's hidden state makes that token's output NaN (the
+    clamp keeps NaN, as torch.clamp does) and leaves the others exact."""
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16
+    g = torch.Generator(device=cuda).manual_seed(93)
+    x, ids, tw = W.moe_w4a16_inputs(4, cuda, g)
+    x[1, 100] = float("nan")
+    d = moe["dev"]
+    log_case("fused moe, NaN in token 1")
+    out = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids)
+    torch.cuda.synchronize()
+    want, _ = run_oracle(oracle, moe, x, ids, tw)
+    w = oracle.bf16_to_f32(want)
+    o = out.float().cpu().numpy()
+    assert np.isnan(w[1]).all() and np.isnan(o[1]).all()
+    keep = [0, 2, 3]
+    assert_out_close(out[keep], want[keep], oracle, "tokens without NaN")
+
+
 def test_graph_replay_deterministic(cuda, moe):
     import torch
     from titan_moe_w4a16 import fused_moe_w4a16
