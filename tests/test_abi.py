@@ -333,3 +333,32 @@ def test_indexer_contract_errors_on_cpu():
         indexer_topk(torch.zeros(2, 100), ctx, 512)
     with pytest.raises(ValueError, match="lengths"):
         indexer_topk(torch.zeros(2, 1000), ctx.long(), 512)
+
+
+def test_topk_plans_keep_their_invariants():
+    """The two-stage top-k's plan (through the workspace size it needs): when
+    it chunks, chunks of 512 * {8, 16, 32} positions, longer than k, at least
+    two of them, and at most 32768 candidates for the final workgroup; rows of
+    at most 4096 columns never chunk."""
+    import _glm53_lib
+    L = _glm53_lib.load()
+    ws = L.glm53_indexer_topk_workspace_bytes
+    for max_len in (1, 100, 4096, 4097, 8191, 20000, 32768, 65536, 65537, 140000, 262144, 1 << 20):
+        for k in (1, 7, 512, 2048, 4095, 4096, 8192, 16384, 32768):
+            if k > max_len:
+                assert ws(3, max_len, k) == 0
+                continue
+            b = ws(3, max_len, k)
+            if max_len <= 4096:
+                assert b == 0, (max_len, k)
+                continue
+            if b == 0:
+                continue   # one workgroup over the row, or the sweeping kernel
+            per_row = b / 3 / 8 / k          # candidates slots = chunks (rounded workspace aside)
+            ok = False
+            for p in (8, 16, 32):
+                chunk = 512 * p
+                chunks = -(-max_len // chunk)
+                if chunk > k and chunks >= 2 and chunks * k <= 32768 and ws(3, max_len, k) == -(-(3 * chunks * k * 8) // 256) * 256:
+                    ok = True
+            assert ok, (max_len, k, per_row)

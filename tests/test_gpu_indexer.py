@@ -249,6 +249,28 @@ def test_logits_nan_codes(cuda, oracle):
     assert np.array_equal(top.cpu().numpy(), oracle.indexer_topk(g0.numpy(), lens.cpu().numpy(), 512))
 
 
+def test_topk_random_shapes(cuda, oracle):
+    """Seeded random row counts, row lengths, k and lengths (every plan
+    appears), each against the oracle's selection."""
+    import torch
+    from sparse_indexer import indexer_topk
+    rng = np.random.default_rng(2026)
+    g = torch.Generator(device=cuda).manual_seed(2026)
+    for case in range(24):
+        n = int(rng.choice([rng.integers(1, 5000), rng.integers(5000, 40000), rng.integers(40000, 150000)]))
+        k = int(rng.integers(1, min(n, 20000) + 1))
+        rows = int(rng.integers(1, 5))
+        x = torch.randn(rows, n, generator=g, device=cuda)
+        if case % 3 == 1:
+            x = torch.round(x * 2)                      # many ties
+        lens = torch.from_numpy(rng.integers(-2, n + 3, size=rows).astype(np.int32)).to(cuda)
+        log_case("indexer top-k random", case, rows, n, k)
+        got = indexer_topk(x, lens, k)
+        torch.cuda.synchronize()
+        want = oracle.indexer_topk(x.cpu().numpy(), lens.cpu().numpy(), k)
+        assert np.array_equal(got.cpu().numpy(), want), (case, rows, n, k)
+
+
 def test_decode_graph_replay(cuda, decode_b8):
     import torch
     from sparse_indexer import indexer_decode_pool_topk
