@@ -91,7 +91,7 @@ __device__ __forceinline__ float row_sum4(float v) {
 struct Group {
   uint4 kd[2];
   float sc;    // the key's scale (meaningful when kok)
-  bool live;   // the group's first page is in the cache (uniform)
+  bool live;   // the group is computed: its page is in the cache (aligned), always (straddling)
   bool kok;    // this lane's key is valid and its page in the cache
 };
 
@@ -99,11 +99,13 @@ template <bool kAligned>
 __device__ __forceinline__ void load_group(const LogitsArgs& a, int t, int j0, int blk, int len, int g, int c,
                                            Group& gr) {
   const int j = j0 + c;
-  gr.live = blk >= 0 && blk < a.num_blocks;
   const int jb = j < len ? j : j0;
   int bj = blk;
-  if (!kAligned && gr.live && jb / a.block_size != j0 / a.block_size) bj = a.bt[t * a.bt_stride + jb / a.block_size];
-  const bool ok = gr.live && bj >= 0 && bj < a.num_blocks;
+  if (!kAligned && jb / a.block_size != j0 / a.block_size) bj = a.bt[t * a.bt_stride + jb / a.block_size];
+  // aligned: the group shares one page, valid or not; straddling: each key
+  // has its own page, so the group is computed whatever its first page is
+  gr.live = !kAligned || (blk >= 0 && blk < a.num_blocks);
+  const bool ok = bj >= 0 && bj < a.num_blocks;
   // The loads are issued on every path (page 0 stands in for a page outside
   // the cache), so the count of loads in flight is the same on all paths
   // and a wait for one group never drains the later groups' loads.

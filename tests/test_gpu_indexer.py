@@ -83,6 +83,7 @@ def test_logits_block_sizes_and_mtp(cuda, oracle):
     for bs in (8, 24, 100):
         cache, nb = W.indexer_cache(cuda, g, 2 * 600, bs)
         bt = torch.randperm(nb, generator=g, device=cuda).to(torch.int32)[: 2 * (nb // 2)].view(2, -1).contiguous()
+        bt[0, 2] = -1     # a group whose first keys sit on this page and the rest on the next (valid) one
         q = (torch.randn(2, 2, 32, 128, generator=g, device=cuda) * 100).to(torch.float8_e4m3fn)
         w = torch.randn(4, 32, generator=g, device=cuda) / 32 ** 0.5
         lens = torch.tensor([599, 313], dtype=torch.int32, device=cuda)
@@ -247,6 +248,37 @@ def test_logits_nan_codes(cuda, oracle):
     top = indexer_topk(got, lens, 512)
     torch.cuda.synchronize()
     assert np.array_equal(top.cpu().numpy(), oracle.indexer_topk(g0.numpy(), lens.cpu().numpy(), 512))
+
+
+def test_logits_random_shapes(cuda, oracle):
+    """Seeded random batch, next_n, heads, block sizes (straddling and not),
+    page padding, contexts, table entries outside the cache, clean or not."""
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits
+    rng = np.random.default_rng(77)
+    g = torch.Generator(device=cuda).manual_seed(77)
+    for case in range(10):
+        B, next_n = int(rng.integers(1, 5)), int(rng.choice([1, 2]))
+        H = int(rng.choice([16, 32, 48, 64]))
+        bs = int(rng.choice([8, 16, 24, 64, 100, 128]))
+        per_req = int(rng.integers(1, 6000 // bs + 2))
+        cache, nb = W.indexer_cache(cuda, g, B * per_req * bs, bs, page_pad=int(rng.choice([0, 48])))
+        bt = torch.randperm(nb, generator=g, device=cuda).to(torch.int32)[: B * per_req].view(B, per_req).contiguous()
+        for r in range(B):
+            if rng.random() < 0.4:
+                bt[r, int(rng.integers(0, per_req))] = int(rng.choice([-1, nb, nb + 7]))
+        q = (torch.randn(B, next_n, H, 128, generator=g, device=cuda) * 80).to(torch.float8_e4m3fn)
+        w = torch.randn(B * next_n, H, generator=g, device=cuda) / H ** 0.5
+        ctx = torch.from_numpy(rng.integers(0, per_req * bs + 40, size=B).astype(np.int32)).to(cuda)
+        max_len = per_req * bs + int(rng.integers(0, 70))
+        clean = bool(rng.random() < 0.5)
+        log_case("indexer logits random", case, B, next_n, H, bs, per_req, max_len, clean)
+        got = fp8_paged_mqa_logits(q, cache, w, ctx, bt, max_len, clean_logits=clean)
+        torch.cuda.synchronize()
+        offs = np.arange(next_n) - (next_n - 1)
+        rows_ctx = (ctx.cpu().numpy()[:, None] + offs[None, :]).reshape(-1)
+        check_logits(oracle, got, q.view(B * next_n, 1, H, 128), cache, w, torch.from_numpy(rows_ctx),
+                     bt.repeat_interleave(next_n, 0), max_len, clean)
 
 
 def test_topk_random_shapes(cuda, oracle):
