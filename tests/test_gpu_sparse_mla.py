@@ -195,6 +195,36 @@ def test_head_counts_and_edges(cuda, oracle, small_cache):
     assert empty.shape == (0, 16, 512)
 
 
+def test_random_shapes(cuda, oracle, small_cache):
+    """Seeded random token counts, head counts, top-k, split counts and index
+    sets (pads, out-of-range values both ways, repeated rows), each against
+    the oracle with the kernel's split count."""
+    from titan_mla import triton_mla_sparse_attention, _choose_num_kv_splits_mi355x
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    rng = np.random.default_rng(4242)
+    g = W.gen(cuda, 4242)
+    for case in range(16):
+        T = int(rng.integers(1, 7))
+        heads = int(rng.choice([1, 4, 8, 16, 20, 32]))
+        topk = 32 * int(rng.integers(1, 81))
+        splits = int(rng.choice([0, 1, 2, 3, 5, 8, 17, 40]))
+        q = (torch.randn(T, heads, 512, generator=g, device=cuda) * float(rng.uniform(0.05, 1.5))).to(torch.bfloat16)
+        idx = torch.from_numpy(rng.integers(-40, n + 40, size=(T, 1, topk)).astype(np.int32)).to(cuda)
+        if case % 4 == 1:
+            idx[:, :, topk // 2:] = -1                                  # trailing pads
+        if case % 4 == 2:
+            idx[:, :, : topk // 3] = idx[:, :, :1]                      # one row repeated
+        eff = splits or _choose_num_kv_splits_mi355x(T, -(-heads // 16), topk, 256)
+        log_case("mla random", case, T, heads, topk, splits, eff)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits or None, sm_count=256)
+        torch.cuda.synchronize()
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=eff, groups=GROUPS,
+                                 block_n=BLOCK, lazy=LAZY)
+        compare(out, want, ("random", case, T, heads, topk, eff))
+
+
 @pytest.fixture(scope="module")
 def full_cache(cuda):
     from titan_kv import store_int8
