@@ -127,6 +127,46 @@ def test_paged_attention(cuda, oracle, splits, block_size, page_bytes):
         assert np.all(err <= np.maximum(MAX_ABS, ulp)) and err.mean() <= MEAN_ABS, (t, err.max())
 
 
+def test_paged_random_shapes(cuda):
+    """Seeded random block sizes, page padding, request counts, table widths,
+    request ids, positions (past the table, negative) and split counts: the
+    fused paged attention equals per-token attention over the logically
+    ordered cache bit for bit, and the flat path through the conversion when
+    the page stride is a whole number of rows."""
+    from sparse_utils import flat_kv_row_view, triton_convert_req_index_to_global_index as conv
+    from titan_mla import triton_mla_sparse_attention, triton_mla_sparse_attention_paged
+    rng = np.random.default_rng(515)
+    g = W.gen(cuda, 515)
+    for case in range(10):
+        block_size = int(rng.choice([16, 48, 64, 200, 256, 1024]))
+        pad_units = int(rng.choice([0, 0, 1, 7, 33]))          # extra 16-byte units per page
+        page_bytes = block_size * 528 + 16 * pad_units
+        reqs = int(rng.integers(1, 4))
+        max_blocks = int(rng.integers(1, 12))
+        num_blocks = reqs * max_blocks + int(rng.integers(0, 4))
+        cache, _ = paged_cache(cuda, num_blocks, block_size, page_bytes, seed=600 + case)
+        bt = tables(cuda, reqs, max_blocks, num_blocks, 700 + case)
+        T = int(rng.integers(1, 6))
+        topk = 32 * int(rng.integers(1, 70))
+        splits = int(rng.choice([1, 2, 5, 8]))
+        req = torch.from_numpy(rng.integers(0, reqs, size=T).astype(np.int32)).to(cuda)
+        span = max_blocks * block_size
+        idx = torch.from_numpy(rng.integers(-3, span + 50, size=(T, topk)).astype(np.int32)).to(cuda)
+        log_case("paged random", case, block_size, pad_units, reqs, max_blocks, T, topk, splits)
+        q = torch.randn(T, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+        fused = triton_mla_sparse_attention_paged(q, cache, idx, req, bt, W.SM_SCALE, num_kv_splits=splits)
+        logical = logical_attention(q, cache, torch.where(idx < span, idx, -1), req, bt, splits, W.SM_SCALE)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, logical), case
+        if page_bytes % 528 == 0:
+            rows, stride = flat_kv_row_view(cache, block_size)
+            flat_idx = conv(req, bt, idx, BLOCK_SIZE=block_size, NUM_TOPK_TOKENS=topk, BLOCK_STRIDE_ROWS=stride)
+            two = triton_mla_sparse_attention(q, rows.view(-1, 1, 528), flat_idx.view(T, 1, topk), W.SM_SCALE,
+                                              num_kv_splits=splits)
+            torch.cuda.synchronize()
+            assert torch.equal(fused, two), case
+
+
 def test_paged_table_entries_outside_the_cache_are_masked(cuda):
     """A block-table entry that is not one of the cache's pages (negative or
     too large, e.g. a stale or unused slot) masks its positions."""
