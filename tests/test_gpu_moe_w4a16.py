@@ -173,6 +173,33 @@ def test_clamp_off_row_stride_and_output(cuda, oracle, moe):
     assert not torch.equal(out, clamped)          # 3-sigma inputs push gate/up past 10
 
 
+def test_random_routes_and_limits(cuda, oracle, moe):
+    """Seeded random batch sizes, experts per slot (a token repeating an
+    expert, ids outside [0, 288)), router weights, input scales and clamp
+    limits."""
+    import torch
+    from titan_moe_w4a16 import fused_moe_w4a16
+    rng = np.random.default_rng(9090)
+    g = torch.Generator(device=cuda).manual_seed(9090)
+    d = moe["dev"]
+    for case in range(8):
+        b = int(rng.integers(1, 9))
+        ids = rng.integers(0, 288, size=(b, 8))
+        if case % 3 == 1:
+            ids[rng.random(ids.shape) < 0.2] = rng.choice([-1, 288, 1000])
+        if case % 3 == 2:
+            ids[0, 1] = ids[0, 0]                          # one token routes twice to an expert
+        ids_t = torch.from_numpy(ids.astype(np.int32)).to(cuda)
+        tw = torch.softmax(torch.randn(b, 8, generator=g, device=cuda), dim=1).contiguous()
+        x = (torch.randn(b, 4096, generator=g, device=cuda) * float(rng.uniform(0.2, 3.0))).to(torch.bfloat16)
+        clamp = float(rng.choice([10.0, 7.0, 25.0]))
+        log_case("fused moe random", case, b, clamp)
+        out = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids_t, clamp_limit=clamp)
+        torch.cuda.synchronize()
+        want, _ = run_oracle(oracle, moe, x, ids_t, tw, clamp=clamp)
+        assert_out_close(out, want, oracle, f"random case {case}")
+
+
 def test_nan_token_propagates(cuda, oracle, moe):
     """A NaN in one token's hidden state makes that token's output NaN (the
     clamp keeps NaN, as torch.clamp does) and leaves the others exact."""
