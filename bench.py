@@ -241,6 +241,32 @@ def main():
                               "gbs_cold": round(bytes1 / (us1_cold * 1e-6) / 1e9, 1), "num_kv_splits": s1}
         del graph1
 
+        # ------------------------------------------------------------ layer rotation
+        # Consecutive layers read their own caches: 8 steps per graph cycling
+        # over 4 caches of 262144 rows (552 MB > the 256 MB MALL), so every
+        # step's rows come from HBM, without the single-call launch overhead
+        # the cold figure carries.  Same q and indices per step.
+        rot = []
+        for li in range(3):
+            _, xr, cr, sr = W.decode_cache(dev, seed=W.SEED_BENCH + 300 + li, dist="t3")
+            store_int8(xr, cr, sr)
+            del xr
+            rot.append(cr.view(n_rows, 1, W.ROW_BYTES))
+        torch.cuda.synchronize()
+        for name, q_, idx_, kv_, nbytes in (("decode_b8", q8, idx8, kv8, bytes8), ("decode_b1", q1, idx1, kv1, bytes1)):
+            caches_ = [kv_] + rot
+            grr, _ = capture(torch, lambda: [triton_mla_sparse_attention(q_, c, idx_, W.SM_SCALE,
+                                                                         num_kv_splits=args.splits)
+                                             for c in caches_ + caches_], 1)
+            for _ in range(3):
+                grr.replay()
+            log(f"{name} layer rotation")
+            us_r = timer.replay_loop(grr, max(4, K // 20)) / 8
+            extra[name]["us_per_step_layer_rotation"] = round(us_r, 3)
+            extra[name]["gbs_layer_rotation"] = round(nbytes / (us_r * 1e-6) / 1e9, 1)
+            del grr
+        del rot
+
         # ------------------------------------------------------------ paged decode B=8
         # Request-relative indices: vLLM-style conversion + attention (two
         # launches before the attention's own) against the fused call.
