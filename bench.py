@@ -241,6 +241,28 @@ def main():
                               "gbs_cold": round(bytes1 / (us1_cold * 1e-6) / 1e9, 1), "num_kv_splits": s1}
         del graph1
 
+        # ------------------------------------------------------------ the whole path, B=8
+        # One decode step of the path in one graph: the 8 new tokens' rows
+        # written into the cache (scattered slots), the sparse MLA decode over
+        # it, and the MoE align of the 8 tokens' routes (launch gaps included).
+        gp = W.gen(dev, W.SEED_BENCH + 400)
+        x_new = torch.randn(8, 512, generator=gp, device=dev).to(torch.bfloat16)
+        slots_new = torch.randperm(n_rows, generator=gp, device=dev)[:8]
+        ids_new = W.moe_routes(8, dev, gp)
+
+        def path_step():
+            store_int8(x_new, cache8, slots_new)
+            out = triton_mla_sparse_attention(q8, kv8, idx8, W.SM_SCALE, num_kv_splits=args.splits)
+            titan_moe_align_small(ids_new)
+            return out
+        gps, _ = capture(torch, path_step, args.unroll)
+        for _ in range(3):
+            gps.replay()
+        log("decode path B=8 (write + attention + align)")
+        extra["decode_path_b8_us_per_step"] = round(timer.replay_loop(gps, max(2, K // args.unroll // 2))
+                                                    / args.unroll, 3)
+        del gps
+
         # ------------------------------------------------------------ layer rotation
         # Consecutive layers read their own caches: 8 steps per graph cycling
         # over 4 caches of 262144 rows (552 MB > the 256 MB MALL), so every
