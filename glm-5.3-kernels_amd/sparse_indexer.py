@@ -116,9 +116,14 @@ def indexer_decode_pool_topk(q: torch.Tensor, kv_cache: torch.Tensor, weights: t
                                   clean_logits=False)
     B, next_n = q.shape[0], q.shape[1]
     lens = context_lens.to(torch.int32)
+    cap = block_tables.shape[1] * kv_cache.shape[1]
+    if next_n == 1 and min(max_model_len, cap) >= k:
+        # the top-k clamps each row's length to the columns it is given: the
+        # columns the block table can hold (no separate clamp launch)
+        return indexer_topk(logits[:, :min(max_model_len, cap)], lens.contiguous(), k)
     if next_n > 1:
         offs = torch.arange(next_n, device=lens.device, dtype=torch.int32) - (next_n - 1)
         lens = (lens[:, None] + offs[None, :]).reshape(-1)
     # positions the block table cannot hold were not scored (clean_logits=False)
-    lens = torch.clamp(lens, max=block_tables.shape[1] * kv_cache.shape[1])
+    lens = torch.clamp(lens, max=cap)
     return indexer_topk(logits, lens.to(torch.int32).contiguous(), k)

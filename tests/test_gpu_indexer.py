@@ -216,6 +216,13 @@ def test_decode_pool_topk_mtp_and_table_capacity(cuda, oracle):
     # the logits of those rows against the float64 oracle (scored positions only)
     check_logits(oracle, logits, q.view(6, 1, 32, 128), cache, w, torch.from_numpy(rows_ctx),
                  bt.repeat_interleave(2, 0), max_pools, False)
+    # next_n = 1 (the decode case): the same clamp, applied by narrowing the columns
+    q1, w1 = q[:, 1:].contiguous(), w.view(3, 2, 32)[:, 1].contiguous()
+    got1 = indexer_decode_pool_topk(q1, cache, w1, ctx, bt, max_pools)
+    logits1 = fp8_paged_mqa_logits(q1, cache, w1, ctx, bt, max_pools, clean_logits=False)
+    torch.cuda.synchronize()
+    ctx1 = np.minimum(ctx.cpu().numpy(), per_req * bs)
+    assert np.array_equal(got1.cpu().numpy(), oracle.indexer_topk(logits1.cpu().numpy(), ctx1, 512))
 
 
 def test_logits_nan_codes(cuda, oracle):
