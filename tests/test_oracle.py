@@ -1,15 +1,11 @@
 """Pins the CPU oracle against what fixes it independently of the oracle itself:
 the reference's published known answers, exact rational arithmetic, closed
 forms, independent formulations and mathematical invariants.  CPU only."""
-import json
 import random
 from fractions import Fraction
-from pathlib import Path
 
 import numpy as np
 import pytest
-
-GOLDEN = Path(__file__).resolve().parent / "golden"
 
 # num_tokens_post_padded known answers published by the reference for its
 # GPU correctness run (docs/measurements.json:99-1444, 168 cases over
