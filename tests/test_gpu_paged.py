@@ -233,6 +233,39 @@ def test_expand_pools_matches_oracle(cuda, oracle, pool_size, with_tail, dtype):
     assert got.shape == want.shape and np.array_equal(got.cpu().numpy(), want)
 
 
+def test_expand_and_convert_random_shapes(cuda, oracle):
+    """Seeded random pool counts, pool sizes, lengths and id widths for the
+    expansion, and random block sizes, page rows, tables and positions for the
+    conversion, each bit-exact against the oracle."""
+    from sparse_utils import expand_pools_and_append_tail, triton_convert_req_index_to_global_index as conv
+    rng = np.random.default_rng(8181)
+    for case in range(12):
+        rows, k = int(rng.integers(1, 9)), int(rng.integers(1, 700))
+        pool_size = int(rng.integers(1, 9))
+        dtype = np.int64 if case % 2 else np.int32
+        pools = rng.integers(-5, 40000, size=(rows, k)).astype(dtype)
+        lens = rng.integers(-3, 200000, size=rows).astype(np.int32)
+        log_case("expand random", case, rows, k, pool_size, dtype.__name__)
+        got = expand_pools_and_append_tail(torch.from_numpy(pools).to(cuda), torch.from_numpy(lens).to(cuda),
+                                           pool_size)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), oracle.expand_pools(pools, lens, pool_size)), case
+    for case in range(12):
+        block_size = int(rng.choice([1, 16, 64, 100, 256, 2304]))
+        page_rows = block_size + int(rng.choice([0, 0, 1, 3]))
+        reqs, max_blocks = int(rng.integers(1, 5)), int(rng.integers(1, 30))
+        bt = rng.integers(-2, 5000, size=(reqs, max_blocks)).astype(np.int32)
+        T, topk = int(rng.integers(1, 10)), 32 * int(rng.integers(1, 70))
+        req = rng.integers(-1, reqs + 1, size=T).astype(np.int32)
+        span = max_blocks * block_size
+        idx = rng.integers(-4, span + 40, size=(T, topk)).astype(np.int32)
+        log_case("convert random", case, block_size, page_rows, reqs, max_blocks, T, topk)
+        got = conv(torch.from_numpy(req).to(cuda), torch.from_numpy(bt).to(cuda), torch.from_numpy(idx).to(cuda),
+                   BLOCK_SIZE=block_size, NUM_TOPK_TOKENS=topk, BLOCK_STRIDE_ROWS=page_rows)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), oracle.convert_req_index(req, bt, idx, block_size, page_rows)), case
+
+
 @pytest.mark.parametrize("splits", [1, 8, None])
 @pytest.mark.parametrize("with_tail", [True, False])
 def test_pooled_attention_equals_expand_then_paged(cuda, splits, with_tail):
