@@ -33,10 +33,11 @@
 // lane (l/16, l%16) holds column n = l%16 and rows m = 4*(l/16) + [0, 4), so
 // each lane needs the single scale of its column.
 //
-// Gate/up kernel: one workgroup per (aligner block of 8 route slots, 16
-// intermediate columns); 8 wavefronts split K (128-feature chunks round
-// robin), each issues all of its weight, scale and activation loads before
-// the first MFMA, then the 8 partial tiles are summed in LDS in wave order.
+// Gate/up kernels: the split-K kernel (1..2 tokens) runs one workgroup per
+// (aligner block of 8 route slots, run of 16-column tiles); 8 wavefronts split
+// K, and each tile's 8 partial tiles are summed in LDS in wave order.  The
+// streaming kernel (K = 4096, 4..8 tokens) gives each wavefront a whole tile
+// pair over all of K with a short register ring of weight chunks.
 // Down kernel: one workgroup per (token, 16 output features); wavefront j
 // computes route slot j of the token (its expert's 16 rows over N), the 8
 // weighted results are summed in slot order.  Both kernels are deterministic.
@@ -368,6 +369,168 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
     gate_up_dispatch<false>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col);
 }
 
+// ------------------------------------------------------------------ gate/up, streaming
+// For K = 4096 with enough tile pairs to give every CU a workgroup (B >= 4 at
+// the decode shape): wave w of workgroup (b, g) computes the whole gate/up
+// tile pair kNw * g + w of block b over all of K.  Its codes and scales
+// stream through a ring of kStreamDepth chunks in registers (one chunk is
+// computed while the next kStreamDepth - 1 are in flight), with no workgroup
+// barrier after the activation rows are staged and no reduction across
+// waves, so each wave runs at its own memory pace.  A shallow ring streams
+// best: B=8 layer 49.3 us (split-K kernel) -> 44.4 / 45.1 / 46.5 us with
+// depth 4 / 6 / 8, and 12 or 15 slower again; depths 2-4 are within 2 %.  Same arithmetic per group
+// as the split-K kernel (all four D rows always kept: one code path, so the
+// compiler has no shared conversions to hoist above a branch); the 32 chunk
+// sums are added in chunk order.
+constexpr int kStreamChunks = kMaxHidden / kChunkK;   // 32
+constexpr int kStreamDepth = 3;
+
+struct StreamRing {
+  uint4 kg[kStreamDepth], ku[kStreamDepth];
+  uint2 scg[kStreamDepth], scu[kStreamDepth];
+};
+
+__device__ __forceinline__ void stream_tile(const GateUpArgs& a, const uint16_t* xs, const uint4* wg, const uint4* wu,
+                                            const uint2* sg, const uint2* su, StreamRing& ring, int jt,
+                                            const int (&slot)[kBlock], int lane) {
+  const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
+  const uint32_t mask = nibble_mask();
+  const int col = lane & 15;
+  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < kStreamChunks; c++) {
+    const int r = c % kStreamDepth;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(xs + kChunkK * c + kGroup * i);
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
+      const f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ring.kg[r], i), mask), corr, 0, 0, 0);
+      const f32x4 du = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ring.ku[r], i), mask), corr, 0, 0, 0);
+      const uint32_t pg = i < 2 ? ring.scg[r].x : ring.scg[r].y;
+      const uint32_t pu = i < 2 ? ring.scu[r].x : ring.scu[r].y;
+      const float s_g = __uint_as_float((i & 1) ? (pg & 0xFFFF0000u) : (pg << 16));
+      const float s_u = __uint_as_float((i & 1) ? (pu & 0xFFFF0000u) : (pu << 16));
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        acc_g[rr] = __builtin_fmaf(s_g, dg[rr], acc_g[rr]);
+        acc_u[rr] = __builtin_fmaf(s_u, du[rr], acc_u[rr]);
+      }
+    }
+    if (c + kStreamDepth < kStreamChunks) {   // refill the slot just used (static condition)
+      const int cn = c + kStreamDepth;
+      ring.kg[r] = wg[64 * cn + lane];
+      ring.ku[r] = wu[64 * cn + lane];
+      ring.scg[r] = sg[16 * cn + col];
+      ring.scu[r] = su[16 * cn + col];
+    }
+    // one chunk per scheduling region, its accumulation included: the
+    // accumulators are otherwise only needed at the end, and the instruction
+    // selector would defer every chunk's FMAs there (keeping all MFMA results
+    // live)
+    asm volatile("" : "+v"(acc_g), "+v"(acc_u));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // lane (q, col) holds column col of rows 4q + rr: slots 0..7 sit in q < 2
+  const int q = lane >> 4;
+#pragma unroll
+  for (int rr = 0; rr < 4; rr++) {
+    const int m = 4 * q + rr;
+    int route = a.num_routes;
+#pragma unroll
+    for (int mm = 0; mm < kBlock; mm++)
+      if (m == mm) route = slot[mm];
+    if (q < 2 && route < a.num_routes) {
+      // compare-and-select clamp: a NaN stays NaN (as torch.clamp keeps it)
+      float g = bf16_round(acc_g[rr]);
+      float up = bf16_round(acc_u[rr]);
+      g = g > a.clamp ? a.clamp : g;
+      up = up > a.clamp ? a.clamp : up < -a.clamp ? -a.clamp : up;
+      const float v = g / (1.0f + expf(-g)) * up;
+      a.act[static_cast<int64_t>(route) * a.n_inter + kTileN * jt + col] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+    }
+  }
+}
+
+template <bool kSelfAlign, int kNw>
+__global__ __launch_bounds__(64 * kNw) void moe_w4a16_gate_up_stream_kernel(const GateUpArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t xsh[kBlock][kXStride];
+  const int b = blockIdx.x;
+  const int n_half = a.n_inter / kTileN;
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  const int col = lane & 15;
+  const int R = a.num_routes;
+
+  int slot[kBlock];   // route of each slot of the block (R = padding); wave-uniform
+  int e;
+  if (kSelfAlign) {
+    const bool in = lane < R;
+    const RoutePos rp = align_routes(in ? load_route_id(a.topk_ids, a.ids_i64, lane) : -1, in);
+#pragma unroll
+    for (int m = 0; m < kBlock; m++) {
+      const uint64_t hit = __ballot(rp.valid && rp.pos == kBlock * b + m);
+      slot[m] = hit ? __builtin_ctzll(hit) : R;
+    }
+    e = slot[0] < R ? __builtin_amdgcn_readlane(rp.key, slot[0]) : -1;
+  } else {
+    e = a.expert_ids[b];
+#pragma unroll
+    for (int m = 0; m < kBlock; m++) slot[m] = a.sorted_ids[kBlock * b + m];
+  }
+  if (e < 0 || e >= a.num_experts) return;   // unused block (uniform over the workgroup)
+
+  // Activation rows: wave w stages features (w + kNw * p) * 512 + [0, 512) of
+  // every routed slot with direct global->LDS loads (no registers held while
+  // the weights stream in).  They go out before the weight ring, so waiting
+  // for them is vmcnt(ring loads).
+  constexpr int kXPer = kMaxHidden / (512 * kNw);
+#pragma unroll
+  for (int m = 0; m < kBlock; m++) {
+    if (slot[m] < R) {   // uniform
+      const unsigned r = static_cast<unsigned>(slot[m]);
+      const unsigned tok = a.topk_log2 >= 0 ? r >> a.topk_log2 : r / static_cast<unsigned>(a.topk);
+      const uint16_t* xr = a.x + static_cast<int64_t>(tok) * a.sx;
+#pragma unroll
+      for (int p = 0; p < kXPer; p++)
+        __builtin_amdgcn_global_load_lds(xr + 512 * (w + kNw * p) + 8 * lane, &xsh[m][512 * (w + kNw * p)], 16,
+                                         0, 0);
+    }
+  }
+
+  const int jt = uniform(static_cast<int>(blockIdx.y) * kNw + w);
+  const int jtc = jt < n_half ? jt : n_half - 1;   // waves past the end load a real tile, store nothing
+  const int64_t tg = (static_cast<int64_t>(e) * 2 * n_half + jtc) * kStreamChunks;
+  const int64_t tu = tg + static_cast<int64_t>(n_half) * kStreamChunks;
+  // uniform tile bases (SGPRs); each access adds the lane's 32-bit offset
+  const uint4* wg = a.w13 + tg * 64;
+  const uint4* wu = a.w13 + tu * 64;
+  const uint2* sg = reinterpret_cast<const uint2*>(a.s13 + tg * 64);
+  const uint2* su = reinterpret_cast<const uint2*>(a.s13 + tu * 64);
+  StreamRing ring;
+#pragma unroll
+  for (int c = 0; c < kStreamDepth; c++) {
+    ring.kg[c] = wg[64 * c + lane];
+    ring.ku[c] = wu[64 * c + lane];
+    ring.scg[c] = sg[16 * c + col];
+    ring.scu[c] = su[16 * c + col];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // vmcnt(4 * kStreamDepth): this wave's activation rows have landed in LDS
+  static_assert(4 * kStreamDepth < 64, "vmcnt is 6 bits");
+  constexpr int kRingLoads = 4 * kStreamDepth;
+  __builtin_amdgcn_s_waitcnt((kRingLoads & 15) | ((kRingLoads >> 4) << 14) | (7 << 4) | (15 << 8));
+  lds_barrier();
+
+  int xrow = 0;   // A-operand row of this lane (m = col): unrouted slots and m >= 8 read row 0
+#pragma unroll
+  for (int m = 1; m < kBlock; m++)
+    if ((col & 7) == m && slot[m] < R) xrow = m;
+  const uint16_t* xs = &xsh[xrow][8 * (lane >> 4)];
+  if (jt >= n_half) return;
+  stream_tile(a, xs, wg, wu, sg, su, ring, jt, slot, lane);
+}
+
 // ------------------------------------------------------------------ down
 struct DownArgs {
   const uint16_t* act;      // bf16 [T * topk][N]
@@ -534,8 +697,23 @@ int launch_gate_up(bool self_align, const void* x, int64_t sx, const void* w13, 
                (topk & (topk - 1)) ? -1 : __builtin_ctzll(static_cast<uint64_t>(topk)), static_cast<int>(tpw),
                static_cast<int>(num_experts), static_cast<int>(n_inter), static_cast<int>(hidden), clamp_limit,
                static_cast<uint16_t*>(act)};
-  const dim3 grid(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + tpw - 1) / tpw));
   (void)hipGetLastError();
+  // Streaming variant: K = 4096 and at least ~4 tile pairs per CU.
+  const int64_t pairs = n_half * num_routes;
+  if (hidden == kMaxHidden && pairs >= 4 * num_cus()) {
+    const int nw = pairs >= 8 * num_cus() ? 8 : 4;
+    const dim3 gs(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + nw - 1) / nw));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (nw == 8) {
+      if (self_align) hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<true, 8>), gs, dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<false, 8>), gs, dim3(512), 0, st, a);
+    } else {
+      if (self_align) hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<true, 4>), gs, dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<false, 4>), gs, dim3(256), 0, st, a);
+    }
+    return static_cast<int>(hipGetLastError());
+  }
+  const dim3 grid(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + tpw - 1) / tpw));
   if (self_align)
     hipLaunchKernelGGL(moe_w4a16_gate_up_kernel<true>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
   else
