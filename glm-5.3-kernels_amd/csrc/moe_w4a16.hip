@@ -33,11 +33,12 @@
 // lane (l/16, l%16) holds column n = l%16 and rows m = 4*(l/16) + [0, 4), so
 // each lane needs the single scale of its column.
 //
-// Gate/up kernels: the split-K kernel (1..2 tokens) runs one workgroup per
-// (aligner block of 8 route slots, run of 16-column tiles); 8 wavefronts split
-// K, and each tile's 8 partial tiles are summed in LDS in wave order.  The
-// streaming kernel (K = 4096, 4..8 tokens) gives each wavefront a whole tile
-// pair over all of K with a short register ring of weight chunks.
+// Gate/up kernels: the streaming kernel (K = 4096) gives each wavefront a
+// tile pair (over all of K, or a part of K when there are few tile pairs)
+// with a short register ring of weight chunks; the split-K kernel (other
+// widths) runs one workgroup per (aligner block of 8 route slots, run of
+// 16-column tiles), 8 wavefronts split K, and each tile's 8 partial tiles are
+// summed in LDS in wave order.
 // Down kernel: one workgroup per (token, 16 output features); wavefront j
 // computes route slot j of the token (its expert's 16 rows over N), the 8
 // weighted results are summed in slot order.  Both kernels are deterministic.
@@ -370,18 +371,20 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
 }
 
 // ------------------------------------------------------------------ gate/up, streaming
-// For K = 4096 with enough tile pairs to give every CU a workgroup (B >= 4 at
-// the decode shape): wave w of workgroup (b, g) computes the whole gate/up
-// tile pair kNw * g + w of block b over all of K.  Its codes and scales
-// stream through a ring of kStreamDepth chunks in registers (one chunk is
-// computed while the next kStreamDepth - 1 are in flight), with no workgroup
-// barrier after the activation rows are staged and no reduction across
-// waves, so each wave runs at its own memory pace.  A shallow ring streams
-// best: B=8 layer 49.3 us (split-K kernel) -> 44.4 / 45.1 / 46.5 us with
-// depth 4 / 6 / 8, and 12 or 15 slower again; depths 2-4 are within 2 %.  Same arithmetic per group
-// as the split-K kernel (all four D rows always kept: one code path, so the
-// compiler has no shared conversions to hoist above a branch); the 32 chunk
-// sums are added in chunk order.
+// For K = 4096 (1..8 tokens at the decode shape): the waves of workgroup
+// (b, g) are kTiles tile pairs x kKSplit parts of K, chosen so that about one
+// workgroup per CU covers all tile pairs (8 x 1 at 8 tokens, 4 x 1 at 4, 2 x 4
+// at 2, 1 x 8 at 1).  Wave (tile, part)
+// computes its gate/up tile pair over its 32 / kKSplit chunks of K, streaming
+// codes and scales through a ring of kStreamDepth chunks in registers (one
+// chunk is computed while the next kStreamDepth - 1 are in flight) at its own
+// memory pace: no barrier between the activation staging and the end.  With
+// kKSplit > 1 the parts meet once in LDS and are added in part order.  A
+// shallow ring streams best: B=8 layer 49.3 us (split-K kernel) -> 44.4 /
+// 45.1 / 46.5 us with depth 4 / 6 / 8, and 12 or 15 slower again; depths 2-4
+// are within 2 %.  Same arithmetic per group as the split-K kernel (all four
+// D rows always kept: one code path, so the compiler has no shared
+// conversions to hoist above a branch); a wave adds its chunks in order.
 constexpr int kStreamChunks = kMaxHidden / kChunkK;   // 32
 constexpr int kStreamDepth = 3;
 
@@ -390,19 +393,20 @@ struct StreamRing {
   uint2 scg[kStreamDepth], scu[kStreamDepth];
 };
 
-__device__ __forceinline__ void stream_tile(const GateUpArgs& a, const uint16_t* xs, const uint4* wg, const uint4* wu,
-                                            const uint2* sg, const uint2* su, StreamRing& ring, int jt,
-                                            const int (&slot)[kBlock], int lane) {
+// Chunks [c0, c0 + kCpw) of one tile pair; the ring holds chunks c0.. on entry.
+template <int kCpw>
+__device__ __forceinline__ void stream_chunks(const uint16_t* xs, const uint4* wg, const uint4* wu, const uint2* sg,
+                                              const uint2* su, StreamRing& ring, int c0, int lane, f32x4& acc_g,
+                                              f32x4& acc_u) {
   const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
   const uint32_t mask = nibble_mask();
   const int col = lane & 15;
-  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < kStreamChunks; c++) {
+  for (int c = 0; c < kCpw; c++) {
     const int r = c % kStreamDepth;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(xs + kChunkK * c + kGroup * i);
+      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(xs + kChunkK * (c0 + c) + kGroup * i);
       const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
       const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
       const f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ring.kg[r], i), mask), corr, 0, 0, 0);
@@ -417,8 +421,8 @@ __device__ __forceinline__ void stream_tile(const GateUpArgs& a, const uint16_t*
         acc_u[rr] = __builtin_fmaf(s_u, du[rr], acc_u[rr]);
       }
     }
-    if (c + kStreamDepth < kStreamChunks) {   // refill the slot just used (static condition)
-      const int cn = c + kStreamDepth;
+    if (c + kStreamDepth < kCpw) {   // refill the slot just used (static condition)
+      const int cn = c0 + c + kStreamDepth;
       ring.kg[r] = wg[64 * cn + lane];
       ring.ku[r] = wu[64 * cn + lane];
       ring.scg[r] = sg[16 * cn + col];
@@ -431,8 +435,13 @@ __device__ __forceinline__ void stream_tile(const GateUpArgs& a, const uint16_t*
     asm volatile("" : "+v"(acc_g), "+v"(acc_u));
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// bf16 gate/up, clamp, SiLU-and-multiply and the c2 store of one tile pair.
+__device__ __forceinline__ void stream_finish(const GateUpArgs& a, const f32x4& acc_g, const f32x4& acc_u, int jt,
+                                              const int (&slot)[kBlock], int lane) {
   // lane (q, col) holds column col of rows 4q + rr: slots 0..7 sit in q < 2
-  const int q = lane >> 4;
+  const int q = lane >> 4, col = lane & 15;
 #pragma unroll
   for (int rr = 0; rr < 4; rr++) {
     const int m = 4 * q + rr;
@@ -452,9 +461,15 @@ __device__ __forceinline__ void stream_tile(const GateUpArgs& a, const uint16_t*
   }
 }
 
-template <bool kSelfAlign, int kNw>
-__global__ __launch_bounds__(64 * kNw) void moe_w4a16_gate_up_stream_kernel(const GateUpArgs a) {
+template <bool kSelfAlign, int kTiles, int kKSplit>
+__global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_stream_kernel(const GateUpArgs a) {
+  constexpr int kW = kTiles * kKSplit;             // waves
+  constexpr int kCpw = kStreamChunks / kKSplit;    // chunks per wave
+  constexpr int kXPer = kWaves / kW;               // 512-feature activation pieces staged per wave
+  static_assert(kCpw >= kStreamDepth, "the ring must fit a wave's chunks");
+  static_assert(kW <= kWaves && kWaves % kW == 0, "1, 2, 4 or 8 waves");
   __shared__ __attribute__((aligned(16))) uint16_t xsh[kBlock][kXStride];
+  __shared__ f32x4 red[kKSplit > 1 ? kW : 1][2][64];
   const int b = blockIdx.x;
   const int n_half = a.n_inter / kTileN;
   const int lane = threadIdx.x & 63;
@@ -480,11 +495,10 @@ __global__ __launch_bounds__(64 * kNw) void moe_w4a16_gate_up_stream_kernel(cons
   }
   if (e < 0 || e >= a.num_experts) return;   // unused block (uniform over the workgroup)
 
-  // Activation rows: wave w stages features (w + kNw * p) * 512 + [0, 512) of
+  // Activation rows: wave w stages features 512 (w + kW p) + [0, 512) of
   // every routed slot with direct global->LDS loads (no registers held while
   // the weights stream in).  They go out before the weight ring, so waiting
   // for them is vmcnt(ring loads).
-  constexpr int kXPer = kMaxHidden / (512 * kNw);
 #pragma unroll
   for (int m = 0; m < kBlock; m++) {
     if (slot[m] < R) {   // uniform
@@ -493,12 +507,12 @@ __global__ __launch_bounds__(64 * kNw) void moe_w4a16_gate_up_stream_kernel(cons
       const uint16_t* xr = a.x + static_cast<int64_t>(tok) * a.sx;
 #pragma unroll
       for (int p = 0; p < kXPer; p++)
-        __builtin_amdgcn_global_load_lds(xr + 512 * (w + kNw * p) + 8 * lane, &xsh[m][512 * (w + kNw * p)], 16,
-                                         0, 0);
+        __builtin_amdgcn_global_load_lds(xr + 512 * (w + kW * p) + 8 * lane, &xsh[m][512 * (w + kW * p)], 16, 0, 0);
     }
   }
 
-  const int jt = uniform(static_cast<int>(blockIdx.y) * kNw + w);
+  const int part = w % kKSplit;
+  const int jt = uniform(static_cast<int>(blockIdx.y) * kTiles + w / kKSplit);
   const int jtc = jt < n_half ? jt : n_half - 1;   // waves past the end load a real tile, store nothing
   const int64_t tg = (static_cast<int64_t>(e) * 2 * n_half + jtc) * kStreamChunks;
   const int64_t tu = tg + static_cast<int64_t>(n_half) * kStreamChunks;
@@ -507,13 +521,14 @@ __global__ __launch_bounds__(64 * kNw) void moe_w4a16_gate_up_stream_kernel(cons
   const uint4* wu = a.w13 + tu * 64;
   const uint2* sg = reinterpret_cast<const uint2*>(a.s13 + tg * 64);
   const uint2* su = reinterpret_cast<const uint2*>(a.s13 + tu * 64);
+  const int c0 = part * kCpw;
   StreamRing ring;
 #pragma unroll
   for (int c = 0; c < kStreamDepth; c++) {
-    ring.kg[c] = wg[64 * c + lane];
-    ring.ku[c] = wu[64 * c + lane];
-    ring.scg[c] = sg[16 * c + col];
-    ring.scu[c] = su[16 * c + col];
+    ring.kg[c] = wg[64 * (c0 + c) + lane];
+    ring.ku[c] = wu[64 * (c0 + c) + lane];
+    ring.scg[c] = sg[16 * (c0 + c) + col];
+    ring.scu[c] = su[16 * (c0 + c) + col];
   }
   __builtin_amdgcn_sched_barrier(0);
   // vmcnt(4 * kStreamDepth): this wave's activation rows have landed in LDS
@@ -527,8 +542,24 @@ __global__ __launch_bounds__(64 * kNw) void moe_w4a16_gate_up_stream_kernel(cons
   for (int m = 1; m < kBlock; m++)
     if ((col & 7) == m && slot[m] < R) xrow = m;
   const uint16_t* xs = &xsh[xrow][8 * (lane >> 4)];
-  if (jt >= n_half) return;
-  stream_tile(a, xs, wg, wu, sg, su, ring, jt, slot, lane);
+  f32x4 acc_g = {0.f, 0.f, 0.f, 0.f}, acc_u = {0.f, 0.f, 0.f, 0.f};
+  stream_chunks<kCpw>(xs, wg, wu, sg, su, ring, c0, lane, acc_g, acc_u);
+  if (kKSplit > 1) {   // every wave reaches this barrier, also those past the last tile
+    red[w][0][lane] = acc_g;
+    red[w][1][lane] = acc_u;
+    lds_barrier();
+    if (part != 0) return;
+#pragma unroll
+    for (int k = 1; k < kKSplit; k++) {
+      const f32x4 vg = red[w + k][0][lane], vu = red[w + k][1][lane];
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        acc_g[rr] += vg[rr];
+        acc_u[rr] += vu[rr];
+      }
+    }
+  }
+  if (jt < n_half) stream_finish(a, acc_g, acc_u, jt, slot, lane);
 }
 
 // ------------------------------------------------------------------ down
@@ -698,19 +729,25 @@ int launch_gate_up(bool self_align, const void* x, int64_t sx, const void* w13, 
                static_cast<int>(num_experts), static_cast<int>(n_inter), static_cast<int>(hidden), clamp_limit,
                static_cast<uint16_t*>(act)};
   (void)hipGetLastError();
-  // Streaming variant: K = 4096 and at least ~4 tile pairs per CU.
+  // Streaming variant at K = 4096: kTiles tile pairs per workgroup so that
+  // about one workgroup per CU covers them; at 1 and 2 tokens 8 and 4 waves
+  // split each pair's K (interleaved A/B against the split-K kernel: B=1
+  // layer 12.1 -> 11.7 us, B=2 18.7 -> 16.8 us; at 4 tokens the 4 x 2 form
+  // was 0.8 us slower than 4 x 1).
   const int64_t pairs = n_half * num_routes;
-  if (hidden == kMaxHidden && pairs >= 4 * num_cus()) {
-    const int nw = pairs >= 8 * num_cus() ? 8 : 4;
-    const dim3 gs(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + nw - 1) / nw));
+  if (hidden == kMaxHidden && pairs >= num_cus()) {
+    const int tiles = pairs >= 8 * num_cus() ? 8 : pairs >= 4 * num_cus() ? 4 : pairs >= 2 * num_cus() ? 2 : 1;
+    const dim3 gs(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + tiles - 1) / tiles));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (nw == 8) {
-      if (self_align) hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<true, 8>), gs, dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<false, 8>), gs, dim3(512), 0, st, a);
-    } else {
-      if (self_align) hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<true, 4>), gs, dim3(256), 0, st, a);
-      else hipLaunchKernelGGL((moe_w4a16_gate_up_stream_kernel<false, 4>), gs, dim3(256), 0, st, a);
-    }
+    auto go = [&](auto kernel, int waves) { hipLaunchKernelGGL(kernel, gs, dim3(64 * waves), 0, st, a); };
+    if (tiles == 8)
+      self_align ? go(moe_w4a16_gate_up_stream_kernel<true, 8, 1>, 8) : go(moe_w4a16_gate_up_stream_kernel<false, 8, 1>, 8);
+    else if (tiles == 4)
+      self_align ? go(moe_w4a16_gate_up_stream_kernel<true, 4, 1>, 4) : go(moe_w4a16_gate_up_stream_kernel<false, 4, 1>, 4);
+    else if (tiles == 2)
+      self_align ? go(moe_w4a16_gate_up_stream_kernel<true, 2, 4>, 8) : go(moe_w4a16_gate_up_stream_kernel<false, 2, 4>, 8);
+    else
+      self_align ? go(moe_w4a16_gate_up_stream_kernel<true, 1, 8>, 8) : go(moe_w4a16_gate_up_stream_kernel<false, 1, 8>, 8);
     return static_cast<int>(hipGetLastError());
   }
   const dim3 grid(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + tpw - 1) / tpw));
