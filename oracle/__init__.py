@@ -1,7 +1,8 @@
 """CPU oracle for the GLM-5.3 decode hot path.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-CPU-baseline leg of bench.py, always as the checker.  The product modules
+CPU-baseline leg of bench.py, always as the reference results are compared
+against (never as the thing measured or shipped).  The product modules
 (titan_kv, titan_mla, titan_moe_align, titan_moe_w4a16, sparse_utils,
 sparse_indexer) never import it.
 
