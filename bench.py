@@ -108,7 +108,7 @@ def main():
                     help="run only a 256 MiB device copy (the HBM byte-counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build runs the hot path at the per-rank shape on a "
+        print("bench.py measures one GPU: the library runs the hot path at the per-rank shape on a "
               "single MI355X; multi-GPU runs are not part of it.", file=sys.stderr)
         sys.exit(2)
     if args.steps < 1 or args.warmup < 0 or args.unroll < 1 or args.steps % args.unroll:

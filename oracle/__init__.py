@@ -55,7 +55,8 @@ Pinning (what each function is checked against, in tests/test_oracle.py):
   (consumed at integration/patch_indexer_sharding.py:58-79): brute-force
   selection on normal, tied, short and special-value rows
   (tests/test_oracle_indexer.py).  The order inside ties (smaller position
-  first, NaN below -inf) is this build's definition.
+  first, NaN below -inf) is this library's definition (vLLM's tie order is
+  not part of the reference).
 """
 from __future__ import annotations
 
