@@ -105,7 +105,7 @@ def test_fused_matches_oracle(cuda, oracle, moe, batch, pattern):
         assert not out.float().abs().sum().item()
 
 
-@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
 def test_gate_up_activation_matches_oracle(cuda, oracle, moe, batch):
     """The first kernel alone, fed by the aligner: c2 of every routed slot."""
     import torch
