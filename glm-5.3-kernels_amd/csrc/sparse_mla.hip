@@ -226,9 +226,20 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   constexpr bool kPaged = kMode != kFlatRows;
   __shared__ MlaShared sh;
 
-  const int split = blockIdx.x;
-  const int t = blockIdx.y;
-  const int hg = blockIdx.z;
+  // Workgroups go to the 8 XCDs round robin by linear id; numbering the
+  // (token, head group) units fastest puts all splits of a unit on one XCD
+  // when there are a multiple of 8 units (B=8: token t on XCD t), where the
+  // merge kernel reads them back.
+  // (Other unit counts keep the plain mapping: the divisions cost B=1
+  // 0.35 us for nothing.)
+  int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
+  if ((gridDim.y * gridDim.z) % 8 == 0) {
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int units = gridDim.y * gridDim.z;
+    split = lin / units;
+    t = (lin % units) % gridDim.y;
+    hg = (lin % units) / gridDim.y;
+  }
   const int w = uniform(threadIdx.x >> 6);
   const int sl = w & (kSlices - 1);
   const int kg = w / kSlices;
@@ -592,9 +603,16 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
   __shared__ float red_m[256 / 64];
   __shared__ float part_den[kMergeLanes];
   __shared__ __attribute__((aligned(16))) float4 part_sum[kMergeLanes][32];
-  const int t = blockIdx.x / num_heads;
-  const int h = blockIdx.x % num_heads;
-  const int quarter = blockIdx.y;
+  // token fastest in the linear id: with a multiple of 8 tokens, token t's
+  // workgroups share the XCD that ran its splits
+  const int num_tokens = gridDim.x / num_heads;
+  int t = blockIdx.x / num_heads, h = blockIdx.x % num_heads, quarter = blockIdx.y;
+  if (num_tokens % 8 == 0) {
+    const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+    t = lin % num_tokens;
+    h = (lin / num_tokens) % num_heads;
+    quarter = lin / (num_tokens * num_heads);
+  }
   const int tid = threadIdx.x;
   const int sl = tid >> 5;          // split lane
   const int ch = tid & 31;          // 4-latent chunk in the quarter
