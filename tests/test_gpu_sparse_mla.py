@@ -225,6 +225,30 @@ def test_random_shapes(cuda, oracle, small_cache):
         compare(out, want, ("random", case, T, heads, topk, eff))
 
 
+def test_xcd_grouped_units(cuda, oracle, small_cache):
+    """Unit counts (tokens x head groups) that are a multiple of 8 take the
+    XCD-grouped workgroup numbering in the split and merge kernels: 8 tokens
+    x 1 group, 4 tokens x 2 groups (32 heads), 8 tokens x 4 groups (64
+    heads) and 16 tokens x 1 group, each with several splits, against the
+    oracle; 20 heads (padded group) at 8 tokens too."""
+    from titan_mla import triton_mla_sparse_attention
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    rng = np.random.default_rng(808)
+    g = W.gen(cuda, 808)
+    for T, heads, topk, splits in ((8, 16, 2176, 17), (4, 32, 1024, 8), (8, 64, 512, 4), (16, 16, 640, 5),
+                                   (8, 20, 896, 7)):
+        q = torch.randn(T, heads, 512, generator=g, device=cuda).to(torch.bfloat16)
+        idx = torch.from_numpy(rng.integers(-8, n + 8, size=(T, 1, topk)).astype(np.int32)).to(cuda)
+        log_case("mla xcd-grouped", T, heads, topk, splits)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+        torch.cuda.synchronize()
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS,
+                                 block_n=BLOCK, lazy=LAZY)
+        compare(out, want, ("xcd-grouped", T, heads, topk, splits))
+
+
 @pytest.fixture(scope="module")
 def full_cache(cuda):
     from titan_kv import store_int8
