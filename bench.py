@@ -66,6 +66,10 @@ class Timer:
         torch.cuda.synchronize()
         return s.elapsed_time(e) * 1e3 / k          # us per replay
 
+    def median_loop(self, graph, k: int, samples: int = 5) -> float:
+        """Median over `samples` timings of k replays (us per replay)."""
+        return statistics.median(self.replay_loop(graph, k) for _ in range(samples))
+
     def cold_loop(self, graph, k: int, flush) -> float:
         torch = self.torch
         evs = []
@@ -81,6 +85,17 @@ class Timer:
         return statistics.median(s.elapsed_time(e) * 1e3 for s, e in evs)
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (as lscpu prints it), from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def capture(torch, fn, unroll: int = 1):
     fn()
     torch.cuda.synchronize()
@@ -92,12 +107,51 @@ def capture(torch, fn, unroll: int = 1):
     return g, out
 
 
+def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
+    """One workload alone, for kernel profiles (rocprofv3 --kernel-trace /
+    --pmc over exactly these dispatches)."""
+    from titan_kv import store_int8
+    from titan_mla import triton_mla_sparse_attention, sparse_mla_partials, _choose_num_kv_splits_mi355x
+    K, unroll = args.steps, args.unroll
+    if args.case == "writer_scattered":
+        # the prefill-shaped call's write: 2048 rows -> randperm slots of a 262144-row cache
+        _, _, new_rows, slots = W.prefill_inputs(dev, g8)
+        fn = lambda: store_int8(new_rows, cache8, slots)
+        nbytes = W.writer_bytes(new_rows.shape[0])
+    elif args.case == "prefill":
+        qp, idxp, _, _ = W.prefill_inputs(dev, g8)
+        fn = lambda: triton_mla_sparse_attention(qp, kv8, idxp, W.SM_SCALE, num_kv_splits=args.splits)
+        nbytes = W.mla_bytes(idxp, n_rows)
+    elif args.case == "decode_b1":
+        g1, x1, cache1, slots1 = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
+        store_int8(x1, cache1, slots1)
+        del x1
+        q1, idx1 = W.decode_b1_inputs(dev, g1)
+        kv1 = cache1.view(n_rows, 1, W.ROW_BYTES)
+        fn = lambda: triton_mla_sparse_attention(q1, kv1, idx1, W.SM_SCALE, num_kv_splits=args.splits)
+        nbytes = W.mla_bytes(idx1, n_rows)
+    else:   # decode_b8_split: the split kernel alone at the auto split count
+        s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
+        fn = lambda: sparse_mla_partials(q8, kv8, idx8, W.SM_SCALE, s8)
+        nbytes = W.mla_bytes(idx8, n_rows)
+    gr, _ = capture(torch, fn, unroll)
+    for _ in range(max(1, args.warmup // unroll)):
+        gr.replay()
+    us = timer.median_loop(gr, max(1, K // unroll)) / unroll
+    log(f"case {args.case}: {us:.3f} us per call, {nbytes / (us * 1e-6) / 1e9:.1f} GB/s algorithmic "
+        f"({nbytes} B), {K} calls, {unroll} per graph")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only: skip extras and CPU baseline")
+    ap.add_argument("--case", choices=("writer_scattered", "prefill", "decode_b1", "decode_b8_split"),
+                    default=None,
+                    help="time one workload alone (K calls, one per graph replay unless --unroll), print "
+                         "its figure to stderr and exit: the command behind a kernel profile")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--splits", type=int, default=None, help="force num_kv_splits for the decode calls")
     ap.add_argument("--sweep", action="store_true",
@@ -153,6 +207,10 @@ def main():
     q8, idx8 = W.decode_b8_inputs(dev, g8)
     del x8
 
+    if args.case:
+        run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu)
+        return
+
     if args.sweep:
         g1s, x1s, cache1s, slots1s = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
         store_int8(x1s, cache1s, slots1s)
@@ -173,32 +231,66 @@ def main():
         return
 
     # ---------------------------------------------------------------- headline: B=8
-    def mla_b8():
-        return triton_mla_sparse_attention(q8, kv8, idx8, W.SM_SCALE, num_kv_splits=args.splits)
+    # HBM-resident (the headline): consecutive steps read different layers'
+    # caches, as a model's layers do -- 5 caches of 262144 rows (692 MB, more
+    # than the 256 MB MALL) cycled within each captured graph, same q and
+    # indices per step.  Warm (one cache replayed, MALL-resident, the
+    # reference's protocol) is reported beside it.
+    log("building 4 more 262144-row caches for the layer rotation")
+    rot = [kv8]
+    for li in range(4):
+        _, xr, cr, sr = W.decode_cache(dev, seed=W.SEED_BENCH + 300 + li, dist="t3")
+        store_int8(xr, cr, sr)
+        del xr
+        rot.append(cr.view(n_rows, 1, W.ROW_BYTES))
+    torch.cuda.synchronize()
 
+    def rotation(fn):
+        """`unroll` calls of fn(cache), cycling over the rotation caches."""
+        return lambda: [fn(rot[i % len(rot)]) for i in range(args.unroll)]
+
+    def mla_b8(kv=kv8):
+        return triton_mla_sparse_attention(q8, kv, idx8, W.SM_SCALE, num_kv_splits=args.splits)
+
+    from titan_mla import sparse_mla_partials
     s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
+    bytes8 = W.mla_bytes(idx8, n_rows)
+    n_samples = 5
+    graph8r, _ = capture(torch, rotation(mla_b8), 1)
+    for _ in range(max(1, Wm // args.unroll)):
+        graph8r.replay()
+    log(f"decode_b8: timing {n_samples} samples of {K} steps (splits={s8}, {args.unroll} per graph, "
+        f"cycling {len(rot)} caches)")
+    us8 = timer.median_loop(graph8r, K // args.unroll, n_samples) / args.unroll
+    gbs8 = bytes8 / (us8 * 1e-6) / 1e9
+    # the dominant kernel alone (first stage: split attention -> partials), same rotation
+    pgr, _ = capture(torch, rotation(lambda kv: sparse_mla_partials(q8, kv, idx8, W.SM_SCALE, s8)), 1)
+    for _ in range(max(1, Wm // args.unroll)):
+        pgr.replay()
+    us8_kernel = timer.median_loop(pgr, K // args.unroll, n_samples) / args.unroll
+    del graph8r, pgr
+    # warm: one cache replayed (MALL-resident)
     graph8, _ = capture(torch, mla_b8, args.unroll)
     for _ in range(Wm):
         graph8.replay()
-    log(f"decode_b8: timing {K} steps (splits={s8}, {args.unroll} per graph)")
-    us8 = timer.replay_loop(graph8, K // args.unroll) / args.unroll
-    bytes8 = W.mla_bytes(idx8, n_rows)
-    gbs8 = bytes8 / (us8 * 1e-6) / 1e9
-    # the dominant kernel alone (first stage: split attention -> partials)
-    from titan_mla import sparse_mla_partials
+    us8_warm = timer.median_loop(graph8, K // args.unroll, n_samples) / args.unroll
+    del graph8
     pg, _ = capture(torch, lambda: sparse_mla_partials(q8, kv8, idx8, W.SM_SCALE, s8), args.unroll)
     for _ in range(Wm):
         pg.replay()
-    us8_kernel = timer.replay_loop(pg, K // args.unroll) / args.unroll
+    us8_kernel_warm = timer.median_loop(pg, K // args.unroll, n_samples) / args.unroll
     del pg
     g8_1, _ = capture(torch, mla_b8, 1)
     us8_cold = timer.cold_loop(g8_1, min(K, 50), flush)
-    us8_single = timer.replay_loop(g8_1, min(K, 100))
+    us8_single = timer.median_loop(g8_1, min(K, 100), n_samples)
     del g8_1
-    extra["decode_b8"] = {"us_per_step_warm": round(us8, 3), "us_per_step_cold": round(us8_cold, 3),
+    extra["decode_b8"] = {"us_per_step_layer_rotation": round(us8, 3), "us_per_step_warm": round(us8_warm, 3),
+                          "us_per_step_cold": round(us8_cold, 3),
                           "us_per_step_one_call_per_graph": round(us8_single, 3),
-                          "us_split_kernel_alone": round(us8_kernel, 3),
-                          "algorithmic_bytes": bytes8, "gbs_warm": round(gbs8, 1),
+                          "us_split_kernel_alone_layer_rotation": round(us8_kernel, 3),
+                          "us_split_kernel_alone_warm": round(us8_kernel_warm, 3),
+                          "algorithmic_bytes": bytes8, "gbs_layer_rotation": round(gbs8, 1),
+                          "gbs_warm": round(bytes8 / (us8_warm * 1e-6) / 1e9, 1),
                           "gbs_cold": round(bytes8 / (us8_cold * 1e-6) / 1e9, 1), "num_kv_splits": s8,
                           "flops": W.mla_flops(idx8, n_rows)}
 
@@ -229,10 +321,10 @@ def main():
         for _ in range(Wm):
             graph1.replay()
         log("decode_b1")
-        us1 = timer.replay_loop(graph1, K // args.unroll) / args.unroll
+        us1 = timer.median_loop(graph1, K // args.unroll) / args.unroll
         g1_1, _ = capture(torch, mla_b1, 1)
         us1_cold = timer.cold_loop(g1_1, min(K, 50), flush)
-        us1_single = timer.replay_loop(g1_1, min(K, 100))
+        us1_single = timer.median_loop(g1_1, min(K, 100))
         del g1_1
         bytes1 = W.mla_bytes(idx1, n_rows)
         extra["decode_b1"] = {"us_per_step_warm": round(us1, 3), "us_per_step_cold": round(us1_cold, 3),
@@ -263,31 +355,19 @@ def main():
                                                     / args.unroll, 3)
         del gps
 
-        # ------------------------------------------------------------ layer rotation
-        # Consecutive layers read their own caches: 8 steps per graph cycling
-        # over 4 caches of 262144 rows (552 MB > the 256 MB MALL), so every
-        # step's rows come from HBM, without the single-call launch overhead
-        # the cold figure carries.  Same q and indices per step.
-        rot = []
-        for li in range(3):
-            _, xr, cr, sr = W.decode_cache(dev, seed=W.SEED_BENCH + 300 + li, dist="t3")
-            store_int8(xr, cr, sr)
-            del xr
-            rot.append(cr.view(n_rows, 1, W.ROW_BYTES))
-        torch.cuda.synchronize()
-        for name, q_, idx_, kv_, nbytes in (("decode_b8", q8, idx8, kv8, bytes8), ("decode_b1", q1, idx1, kv1, bytes1)):
-            caches_ = [kv_] + rot
-            grr, _ = capture(torch, lambda: [triton_mla_sparse_attention(q_, c, idx_, W.SM_SCALE,
-                                                                         num_kv_splits=args.splits)
-                                             for c in caches_ + caches_], 1)
-            for _ in range(3):
-                grr.replay()
-            log(f"{name} layer rotation")
-            us_r = timer.replay_loop(grr, max(4, K // 20)) / 8
-            extra[name]["us_per_step_layer_rotation"] = round(us_r, 3)
-            extra[name]["gbs_layer_rotation"] = round(nbytes / (us_r * 1e-6) / 1e9, 1)
-            del grr
-        del rot
+        # ------------------------------------------------------------ B=1 layer rotation
+        # B=1 over its own cache and the four rotation caches (HBM-resident).
+        rot1 = [kv1] + rot[1:]
+        grr, _ = capture(torch, lambda: [triton_mla_sparse_attention(q1, rot1[i % len(rot1)], idx1, W.SM_SCALE,
+                                                                     num_kv_splits=args.splits)
+                                         for i in range(args.unroll)], 1)
+        for _ in range(3):
+            grr.replay()
+        log("decode_b1 layer rotation")
+        us_r = timer.median_loop(grr, max(1, K // args.unroll)) / args.unroll
+        extra["decode_b1"]["us_per_step_layer_rotation"] = round(us_r, 3)
+        extra["decode_b1"]["gbs_layer_rotation"] = round(bytes1 / (us_r * 1e-6) / 1e9, 1)
+        del grr, rot1
 
         # ------------------------------------------------------------ paged decode B=8
         # Request-relative indices: vLLM-style conversion + attention (two
@@ -358,6 +438,15 @@ def main():
             moe[f"B{b}"] = round(statistics.median(samples), 3)
             del mg
         extra["moe_align_us_per_call"] = moe
+        # The dispatch floor of the same protocol: a kernel adding 1 to one
+        # int32, 16 per graph.
+        one = torch.zeros(1, dtype=torch.int32, device=dev)
+        fg, _ = capture(torch, lambda: one.add_(1), unroll=16)
+        for _ in range(5):
+            fg.replay()
+        extra["graph_dispatch_floor_us_per_kernel"] = round(
+            statistics.median(timer.replay_loop(fg, 100) / 16 for _ in range(5)), 3)
+        del fg, one
         extra["moe_align_reference_us_per_call_sm80"] = {"B1": 1.63, "B2": 1.97, "B4": 1.97, "B8": 5.07}
 
         # ------------------------------------------------------------ MoE W4A16 layer
@@ -382,9 +471,9 @@ def main():
                 xm, idm, twm = W.moe_w4a16_inputs(b, dev, gmw)
                 calls.append((xm, idm, twm, layers[i % 4]))
             one = lambda c=calls[0]: fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1])
-            rot = lambda: [fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1]) for c in calls]
+            rot_moe = lambda: [fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1]) for c in calls]
             gw, _ = capture(torch, one, args.unroll)
-            gr, _ = capture(torch, rot, 1)
+            gr, _ = capture(torch, rot_moe, 1)
             for _ in range(3):
                 gw.replay()
                 gr.replay()
@@ -442,22 +531,37 @@ def main():
         extra["indexer_decode"] = idx
 
         # ------------------------------------------------------------ prefill-shaped
+        # T=2048 tokens, one split.  warm: one cache replayed (138 MB, MALL-
+        # resident); rotation: consecutive calls over 3 caches (415 MB, read
+        # from HBM).
         qp, idxp, new_rows, pslots = W.prefill_inputs(dev, g8)
         pg, _ = capture(torch, lambda: triton_mla_sparse_attention(qp, kv8, idxp, W.SM_SCALE))
         pg.replay()
         log("prefill T=2048")
-        us_p = timer.replay_loop(pg, 5)
+        us_p = timer.median_loop(pg, 5)
+        del pg
+        pgr, _ = capture(torch, lambda: [triton_mla_sparse_attention(qp, c, idxp, W.SM_SCALE) for c in rot[:3]])
+        pgr.replay()
+        us_pr = timer.median_loop(pgr, 3) / 3
+        del pgr
         bytes_p = W.mla_bytes(idxp, n_rows)
         flops_p = W.mla_flops(idxp, n_rows)
-        extra["prefill_t2048"] = {"us_per_call": round(us_p, 1), "algorithmic_bytes": bytes_p,
-                                  "gbs": round(bytes_p / (us_p * 1e-6) / 1e9, 1),
-                                  "tflops": round(flops_p / (us_p * 1e-6) / 1e12, 2)}
-        del pg
+        extra["prefill_t2048"] = {"us_per_call_warm": round(us_p, 1), "us_per_call_rotation": round(us_pr, 1),
+                                  "algorithmic_bytes": bytes_p,
+                                  "gbs_warm": round(bytes_p / (us_p * 1e-6) / 1e9, 1),
+                                  "gbs_rotation": round(bytes_p / (us_pr * 1e-6) / 1e9, 1),
+                                  "hbm_frac_rotation": round(bytes_p / (us_pr * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+                                  "tflops_warm": round(flops_p / (us_p * 1e-6) / 1e12, 2)}
+        # the prefill-shaped call's write: 2048 rows into randperm slots,
+        # `unroll` calls per graph (one call per graph would time the graph
+        # launch, ~15 us, not the kernel's ~3 us)
         c5 = torch.zeros_like(cache8)
-        wpg, _ = capture(torch, lambda: store_int8(new_rows, c5, pslots))
-        us_ws = timer.replay_loop(wpg, 50)
+        wpg, _ = capture(torch, lambda: store_int8(new_rows, c5, pslots), args.unroll)
+        wpg.replay()
+        us_ws = timer.median_loop(wpg, max(2, K // args.unroll)) / args.unroll
         extra["store_int8_2048_scattered"] = {"us_per_call": round(us_ws, 2),
-                                              "gbs": round(W.writer_bytes(2048) / (us_ws * 1e-6) / 1e9, 1)}
+                                              "gbs": round(W.writer_bytes(2048) / (us_ws * 1e-6) / 1e9, 1),
+                                              "calls_per_graph": args.unroll}
         del wpg, c5
 
         # ------------------------------------------------------------ CPU baseline
@@ -523,19 +627,30 @@ def main():
             extra["cpu_oracle_rows"] = rows_cpu
 
     # dominant kernel: sparse_mla_kernel (split attention); algorithmic bytes of
-    # the step over its event-timed average duration.  traffic: measured HBM-side
-    # bytes per dispatch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated).
+    # the step over its event-timed average duration in the same HBM-resident
+    # rotation.  traffic: measured HBM-side bytes per dispatch (rocprofv3
+    # FETCH_SIZE + WRITE_SIZE, copy-calibrated), keyed by kernel and grid
+    # (workgroups x threads): a grid with no committed measurement gives null
+    # and says so.
     ach = bytes8 / (us8_kernel * 1e-6) / 1e9
-    traffic = None
+    traffic, traffic_note = None, None
+    key = f"sparse_mla_kernel@{s8 * 8 * 512}"
     tf = ROOT / "profiles" / "hbm_bytes_per_dispatch.json"
-    if tf.exists() and args.splits in (None, s8):
-        d = json.loads(tf.read_text())["per_dispatch"].get(f"sparse_mla_kernel@{s8 * 8 * 512}")
-        if d:
-            traffic = d["fetch_bytes"] + d["write_bytes"]
+    d = json.loads(tf.read_text())["per_dispatch"].get(key) if tf.exists() else None
+    if d:
+        traffic = d["fetch_bytes"] + d["write_bytes"]
+    else:
+        traffic_note = f"no HBM byte measurement for {key} in {tf.relative_to(ROOT)}"
+        log(f"WARNING: roofline.traffic is null: {traffic_note}")
     roofline = {"bound": "hbm", "kernel": "sparse_mla_kernel", "achieved": round(ach, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "algorithmic_bytes": bytes8,
-                "avg_kernel_us": round(us8_kernel, 3)}
+                "avg_kernel_us": round(us8_kernel, 3),
+                "timing": f"median of {n_samples} samples of {K} launches, HBM-resident (layer rotation)"}
+    if traffic_note:
+        roofline["traffic_note"] = traffic_note
+    if cpu is not None:
+        cpu["cpu_model"] = cpu_model()
     line = {
         "metric": METRIC,
         "value": round(gbs8, 1),
@@ -552,7 +667,11 @@ def main():
         "config": {"workload": "decode_b8: sparse NoPE MLA decode, B=8, 16 heads, 262144-row INT8 cache, "
                                "2176 indices/query (locality-biased, 0-256 trailing pads), Student-t latents",
                    "batch": 8, "context": n_rows, "topk": W.TOPK, "heads": 16, "num_kv_splits": s8,
-                   "timing": f"HIP graph replay, {args.unroll} steps per graph, warm"},
+                   "timing": f"HIP graph replay, {args.unroll} steps per graph, median of {n_samples} samples "
+                             f"of {K} steps",
+                   "residency": f"HBM: consecutive steps cycle over {len(rot)} caches of 262144 rows "
+                                f"({len(rot) * n_rows * W.ROW_BYTES / 1e6:.0f} MB > the 256 MB MALL); "
+                                "the warm (MALL-resident) figure is extra.decode_b8.us_per_step_warm"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "device": {"name": props.name, "cus": cu},

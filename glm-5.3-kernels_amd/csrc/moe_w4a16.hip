@@ -338,20 +338,26 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
   const int k_chunks = a.hidden / kChunkK;
   const int cpw = (k_chunks + kWaves - 1) / kWaves;
   const int c_lo = cpw * w;
+  // A wave whose range starts at or past the end of the row (hidden sizes
+  // that do not fill all waves, e.g. 640 = 5 chunks over 8 waves) computes
+  // nothing and stages nothing: its activation offset would lie past the row.
   const int kbase = kChunkK * c_lo;                 // first feature of this wave
+  const bool stage = kbase < a.hidden;              // uniform over the wave
   const int xo = kbase + 8 * (8 * lane < kChunkK * cpw && kbase + 8 * lane < a.hidden ? lane : 0);
   auto x_row = [&](int route) {
     const unsigned r = static_cast<unsigned>(route);
     const unsigned tok = a.topk_log2 >= 0 ? r >> a.topk_log2 : r / static_cast<unsigned>(a.topk);
     return reinterpret_cast<const uint4*>(a.x + static_cast<int64_t>(tok) * a.sx + xo);
   };
-  const uint4 x0 = *x_row(slot[0]);
+  const uint4 x0 = stage ? *x_row(slot[0]) : make_uint4(0, 0, 0, 0);
   TileRegs t[2];
   load_tile(t[0], a, e, jt0, c_lo, cpw, k_chunks, lane, col);
-  *reinterpret_cast<uint4*>(&sh.x[0][xo]) = x0;
+  if (stage) {
+    *reinterpret_cast<uint4*>(&sh.x[0][xo]) = x0;
 #pragma unroll
-  for (int m = 1; m < kBlock; m++)
-    if (slot[m] < R) *reinterpret_cast<uint4*>(&sh.x[m][xo]) = *x_row(slot[m]);
+    for (int m = 1; m < kBlock; m++)
+      if (slot[m] < R) *reinterpret_cast<uint4*>(&sh.x[m][xo]) = *x_row(slot[m]);
+  }
 
   // A-operand row of this lane (m = col): padding slots and m >= 8 read row 0
   // (their D rows are discarded), so a block with one route reads one row.

@@ -247,7 +247,10 @@ def sparse_mla_f64(q_u16: np.ndarray, rows: np.ndarray, idx: np.ndarray, sm_scal
 
 
 def default_threads() -> int:
-    return len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    """Host threads for the oracle: the CPUs this process may run on, at
+    most 16 (a GPU box's CPU share per GPU)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return max(1, min(16, n))
 
 
 def convert_req_index(req_id: np.ndarray, block_table: np.ndarray, indices: np.ndarray,

@@ -103,6 +103,27 @@ def test_mla_and_writer_contract_assertions_on_cpu():
     assert [_choose_num_kv_splits(t, 1, 2176, 70) for t in (1, 6, 8, 2048)] == [32, 8, 8, 1]
 
 
+def test_library_split_policy_table():
+    """The library's auto split count (_choose_num_kv_splits_mi355x): the
+    largest divisor of topk / 32 with tokens x head groups x splits <= CUs and
+    at least two 32-key tiles per split.  Hand table at 256 CUs."""
+    from titan_mla import _choose_num_kv_splits_mi355x as pick
+    table = {
+        (1, 1, 2176, 256): 34, (2, 1, 2176, 256): 34, (3, 1, 2176, 256): 34, (4, 1, 2176, 256): 34,
+        (8, 1, 2176, 256): 17,            # 8 x 34 > 256: 68 tiles' next divisor down
+        (8, 4, 2176, 256): 4,             # 32 units: 68 = 4 x 17, 32 x 4 = 128 <= 256 < 32 x 17
+        (256, 1, 2176, 256): 1, (2048, 1, 2176, 256): 1,
+        (1, 1, 32, 256): 1,               # one tile: nothing to split
+        (1, 1, 64, 256): 1,               # two tiles: one split keeps both key groups busy
+        (1, 1, 96, 256): 1, (1, 1, 128, 256): 2,
+        (1, 1, 2150, 256): 1,             # not a multiple of 32
+        (1, 1, 16384, 256): 256,          # 512 tiles: 256 splits of 2 (the merge's loop path)
+        (1, 1, 2176, 70): 34,             # 34 <= 70
+        (3, 1, 2176, 70): 17, (0, 1, 2176, 256): 1,
+    }
+    assert {k: pick(*k) for k in table} == table
+
+
 def test_import_does_not_touch_cuda():
     """Mirrors tests/test_cpu_contracts.py:33-53: importing the entry-point
     modules must not query the device."""

@@ -276,24 +276,27 @@ def test_whole_experts_n2048(cuda, oracle):
 
 
 @pytest.mark.gpu
-def test_split_k_kernel_other_width(cuda, oracle):
+@pytest.mark.parametrize("hidden,inter", [(1024, 256), (640, 256), (1536, 128)])
+def test_split_k_kernel_other_width(cuda, oracle, hidden, inter):
     """Hidden sizes other than 4096 take the split-K gate/up kernel (4096
-    streams): hidden 1024 and intermediate 256 with 288 experts at 1, 3 and 8
-    tokens (experts shared between tokens from B=3 on), against the oracle on
-    the experts the routes use."""
+    streams), at 1, 3 and 8 tokens (experts shared between tokens from B=3
+    on), against the oracle on the experts the routes use.  640 (5 chunks of
+    128 over 8 waves) and 1536 (12 chunks, 2 per wave) leave the last waves
+    with no chunk: they must stage no activations (their offset lies past the
+    row) and add nothing."""
     import torch
     from titan_moe_w4a16 import fused_moe_w4a16, repack_w4a16
-    log_case("moe layer K=1024 N=256: build 288 x (512 x 1024 + 1024 x 256) W4A16 weights")
-    lay = W.moe_w4a16_layer(cuda, seed=W.SEED_FIXTURE + 11, hidden=1024, inter=256)
+    log_case(f"moe layer K={hidden} N={inter}: build 288 x ({2 * inter} x {hidden} + {hidden} x {inter}) weights")
+    lay = W.moe_w4a16_layer(cuda, seed=W.SEED_FIXTURE + 11, hidden=hidden, inter=inter)
     w13, s13 = repack_w4a16(lay["w13_packed"], lay["w13_scale"])
     w2, s2 = repack_w4a16(lay["w2_packed"], lay["w2_scale"])
-    g = torch.Generator(device=cuda).manual_seed(1024)
+    g = torch.Generator(device=cuda).manual_seed(hidden)
     bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
     for batch in (1, 3, 8):
-        x, ids, tw = W.moe_w4a16_inputs(batch, cuda, g, hidden=1024)
+        x, ids, tw = W.moe_w4a16_inputs(batch, cuda, g, hidden=hidden)
         if batch > 1:
             ids[1, :3] = ids[0, :3]               # experts shared by two tokens: multi-slot blocks
-        log_case(f"fused moe K=1024 N=256 B={batch}")
+        log_case(f"fused moe K={hidden} N={inter} B={batch}")
         out = fused_moe_w4a16(x, w13, w2, s13, s2, tw, ids)
         torch.cuda.synchronize()
         used = torch.unique(ids.flatten().long())
@@ -302,4 +305,4 @@ def test_split_k_kernel_other_width(cuda, oracle):
         want, _ = oracle.moe_w4a16(bits(x), pick(lay["w13_packed"]).cpu().numpy(), bits(pick(lay["w13_scale"])),
                                    pick(lay["w2_packed"]).cpu().numpy(), bits(pick(lay["w2_scale"])),
                                    tw.cpu().numpy(), local.cpu().numpy())
-        assert_out_close(out, want, oracle, f"K=1024 N=256 B={batch}")
+        assert_out_close(out, want, oracle, f"K={hidden} N={inter} B={batch}")

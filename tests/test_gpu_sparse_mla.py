@@ -1,15 +1,23 @@
 """GPU parity of triton_mla_sparse_attention (HIP) against the CPU oracle.
 
-Bar (BF16 attention output), against the oracle's faithful restatement run
-with the kernel's split count and reduction structure (32-key tiles dealt
-alternately to two key-group streams, merged at the end):
-  per element |err| <= max(2e-2, one bf16 ulp of the reference value), and
-  mean-abs <= 2e-3.
-Below |out| = 4 the per-element bound is exactly 2e-2; above it a single bf16
-rounding flip (any change of fp32 summation order can cause one) is larger
-than 2e-2, so one ulp is allowed there.  Plus the reference's own statistical
-checks against fp32 attention over the original BF16 latents
-(tests/verify_mla.py:71-94) and float64 textbook attention."""
+Bar (BF16 attention output), the north-star one: mean-abs <= 2e-3 and per
+element |err| <= 2e-2, where rare elements with |ref| >= 2 may differ by up to
+two bf16 ulps of the reference value instead (rounding flips; see compare),
+against
+  * the reference's own reduction: one online-softmax stream per split at
+    the reference's autotuned tile widths (BLOCK_N 32 and 64,
+    kernels/titan_mla.py:39-43) and at the split counts the reference picks
+    for these shapes on its 70-SM part (_choose_num_kv_splits: 32 at B=1,
+    8 at B=8, 1 at T=2048), on the benchmark configurations exactly (the
+    16384-row fixture, the 262144-row N(0,1) cache at B=1, the Student-t
+    cache at B=8, all 2048 tokens of the prefill-shaped call); and
+  * the oracle run with the kernel's own split count and reduction structure
+    (32-key tiles dealt alternately to two key-group streams, merged at the
+    end) for the edge cases (odd head counts, empty and oversubscribed
+    splits, random shapes).
+Plus the reference's own statistical checks against fp32 attention over the
+original BF16 latents (tests/verify_mla.py:71-94) and float64 textbook
+attention."""
 import numpy as np
 import pytest
 import torch
@@ -46,15 +54,30 @@ def bf16_ulp(v):
 
 
 def compare(out, want_u16, tag):
+    """mean-abs <= 2e-3 and per element |err| <= 2e-2, except
+    on rare elements (at most max(2, n / 100000)) of magnitude |ref| >= 2,
+    which may differ by up to two bf16 ulps of the reference value: rounding
+    flips of the bf16 output and of a dominant key's bf16(p * scale) operand,
+    which any change of fp32 summation order causes now and then (the
+    reference's own arithmetic dealt to two streams instead of one does it on
+    the CPU: tests/test_oracle.py::test_literal_bar_breaks_under_reordering).
+    Above |ref| = 4 a single ulp is already more than 2e-2."""
     got = out.float().cpu().numpy()
     want = f32(want_u16)
     err = np.abs(got - want)
-    ulps = err / bf16_ulp(want)
+    ulp = bf16_ulp(want)
+    over = err > MAX_ABS
+    n_over = int(over.sum())
+    extra = ""
+    if n_over:
+        extra = (f" | {n_over} of {err.size} over 2e-2: |ref| {np.abs(want[over]).min():.3g}.."
+                 f"{np.abs(want[over]).max():.3g}, at most {float((err[over] / ulp[over]).max()):.3g} bf16 ulp")
     print(f"[cmp] {tag}: max|ref| {np.abs(want).max():.3g} max-abs {err.max():.3g} "
-          f"mean-abs {err.mean():.3g} max-ulp {ulps.max():.3g}", flush=True)
+          f"mean-abs {err.mean():.3g}{extra}", flush=True)
     assert np.isfinite(got).all(), tag
-    bound = np.maximum(MAX_ABS, bf16_ulp(want))
-    assert np.all(err <= bound) and err.mean() <= MEAN_ABS, (tag, float(err.max()), float(err.mean()))
+    assert err.mean() <= MEAN_ABS, (tag, float(err.mean()))
+    assert np.all(err[over] <= 2 * ulp[over]) and np.all(np.abs(want[over]) >= 2), (tag, float(err.max()))
+    assert n_over <= max(2, err.size // 100000), (tag, n_over)
     return float(err.max()), float(err.mean())
 
 
@@ -303,3 +326,126 @@ def test_prefill_shaped_sampled(cuda, oracle, full_cache):
                              groups=GROUPS, block_n=BLOCK, lazy=LAZY)
     got = out[torch.as_tensor(pick, device=cuda)]
     compare(got, want, "prefill sample")
+
+
+# ---------------------------------------------------------------- the reference's own reduction
+
+REF_SM_COUNT = 70        # the reference's part (integration/titan_backend.py:28)
+
+
+def ref_splits(tokens):
+    """The split count the reference's heuristic picks on its own part
+    (kernels/titan_mla.py:432-449): 32 at B=1, 8 at B=8, 1 at T=2048."""
+    from titan_mla import _choose_num_kv_splits
+    return _choose_num_kv_splits(tokens, 1, W.TOPK, REF_SM_COUNT)
+
+
+def check_reference_reduction(oracle, outs, q, rows, idx, tag):
+    """Every GPU output in `outs` against the reference's single-stream
+    reduction at both autotuned tile widths and the reference's split count."""
+    s = ref_splits(q.shape[0])
+    qn, ixn = u16(q), idx.cpu().numpy()
+    for block_n in (32, 64):
+        want = oracle.sparse_mla(qn, rows, ixn, W.SM_SCALE, n_splits=s, groups=1, block_n=block_n,
+                                 nthreads=oracle.default_threads())
+        for name, out in outs.items():
+            compare(out, want, (tag, name, f"reference splits={s} BLOCK_N={block_n}"))
+
+
+def test_reference_reduction_small(cuda, oracle, small_cache):
+    """The 16384-row fixture at B=1 (2048 uniform + 128 pads)."""
+    from titan_mla import triton_mla_sparse_attention
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    log_case("mla small B1 vs the reference reduction")
+    outs = {"auto": triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE),
+            "reference splits": triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE,
+                                                            num_kv_splits=ref_splits(1))}
+    torch.cuda.synchronize()
+    check_reference_reduction(oracle, outs, w["q"], rows, w["idx"], "small B1")
+
+
+@pytest.fixture(scope="module")
+def normal_cache(cuda):
+    """262144 rows of N(0,1) latents: the full-context B=1 configuration."""
+    from titan_kv import store_int8
+    g, x, cache, slots = W.decode_cache(cuda, seed=W.SEED_BENCH + 1, dist="normal")
+    store_int8(x, cache, slots)
+    torch.cuda.synchronize()
+    del x
+    return cache, rows_np(cache)
+
+
+@pytest.mark.slow
+def test_reference_reduction_full_b1(cuda, oracle, normal_cache):
+    """B=1 over the N(0,1) 262144-row cache: 2048 indices uniform over the
+    context, then 128 pads."""
+    from titan_mla import triton_mla_sparse_attention
+    cache, rows = normal_cache
+    kv = cache.view(-1, 1, 528)
+    q, idx = W.decode_b1_inputs(cuda, W.gen(cuda, W.SEED_BENCH + 11))
+    assert int((idx >= 0).sum()) == 2048
+    log_case("mla full B1 N(0,1) vs the reference reduction")
+    outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE),
+            "reference splits": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=ref_splits(1))}
+    torch.cuda.synchronize()
+    check_reference_reduction(oracle, outs, q, rows, idx, "full B1")
+
+
+@pytest.mark.slow
+def test_reference_reduction_full_b8(cuda, oracle, full_cache):
+    """B=8 over the Student-t 262144-row cache, locality-biased indices with
+    0..256 trailing pads per row."""
+    from titan_mla import triton_mla_sparse_attention
+    _, cache = full_cache
+    kv = cache.view(-1, 1, 528)
+    rows = rows_np(cache)
+    q, idx = W.decode_b8_inputs(cuda, W.gen(cuda, W.SEED_BENCH + 18))
+    log_case("mla full B8 Student-t vs the reference reduction")
+    outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE),
+            "reference splits": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=ref_splits(8))}
+    torch.cuda.synchronize()
+    check_reference_reduction(oracle, outs, q, rows, idx, "full B8")
+
+
+@pytest.mark.slow
+def test_reference_reduction_prefill_all_tokens(cuda, oracle, full_cache):
+    """The prefill-shaped call, every one of its 2048 query tokens: causal
+    locality-biased indices over the Student-t cache, one split (the
+    reference's choice and the library's)."""
+    from titan_mla import triton_mla_sparse_attention
+    _, cache = full_cache
+    kv = cache.view(-1, 1, 528)
+    rows = rows_np(cache)
+    q, idx, _, _ = W.prefill_inputs(cuda, W.gen(cuda, W.SEED_BENCH + 2048))
+    assert ref_splits(2048) == 1
+    log_case("mla prefill-shaped T=2048, all tokens, vs the reference reduction")
+    outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE)}
+    torch.cuda.synchronize()
+    check_reference_reduction(oracle, outs, q, rows, idx, "prefill T=2048")
+
+
+def test_merge_beyond_register_splits(cuda, oracle, small_cache):
+    """More than 128 splits take the merge kernel's loop path (the register
+    path holds 128): 200 and 256 splits of a 16384-index top-k (the auto
+    policy's answer at B=1), against the oracle with the same splits, and
+    partials + merge equal to one call bit for bit."""
+    from titan_mla import (triton_mla_sparse_attention, sparse_mla_partials, sparse_mla_merge,
+                           _choose_num_kv_splits_mi355x)
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    g = W.gen(cuda, 16384)
+    q = torch.randn(2, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+    idx = torch.randint(-64, n, (2, 1, 16384), generator=g, device=cuda, dtype=torch.int32)
+    assert _choose_num_kv_splits_mi355x(1, 1, 16384, 256) == 256
+    for s in (200, 256):
+        log_case("mla merge loop path", s)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=s)
+        two = sparse_mla_merge(sparse_mla_partials(q, kv, idx, W.SM_SCALE, s), 2, 16, s)
+        torch.cuda.synchronize()
+        assert torch.equal(out, two), s
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s, groups=GROUPS,
+                                 block_n=BLOCK, lazy=LAZY, nthreads=oracle.default_threads())
+        compare(out, want, ("merge loop path", s))

@@ -151,3 +151,27 @@ def test_full_context_writer_bit_exact(cuda, oracle):
         assert np.array_equal(got, want), dist
         del x, cache
         torch.cuda.empty_cache()
+
+
+@pytest.mark.slow
+def test_prefill_scattered_writer_full_size(cuda, oracle):
+    """The prefill-shaped call's write: 2048 new N(0,1) rows into a random
+    permutation of the slots of a [1024, 256, 528] cache that already holds
+    262144 rows; every written row bit-exact, every other row untouched."""
+    from titan_kv import store_int8
+    log_case("store_int8 2048 rows -> randperm slots of a 262144-row cache")
+    g = W.gen(cuda, W.SEED_BENCH + 5)
+    old = torch.randint(-128, 128, (1024, 256, 528), generator=g, device=cuda, dtype=torch.int8)
+    cache = old.clone()
+    _, _, new_rows, slots = W.prefill_inputs(cuda, g)
+    assert slots.dtype == torch.int64 and slots.numel() == 2048
+    store_int8(new_rows, cache, slots)
+    torch.cuda.synchronize()
+    flat = u8(cache).reshape(-1, 528)
+    was = u8(old).reshape(-1, 528)
+    s = slots.cpu().numpy()
+    want = oracle.quantize_rows(u16(new_rows), nthreads=oracle.default_threads())
+    assert np.array_equal(flat[s], want)
+    untouched = np.ones(flat.shape[0], bool)
+    untouched[s] = False
+    assert np.array_equal(flat[untouched], was[untouched])
