@@ -18,6 +18,7 @@ EXPORTED = (
     "glm53_store_int8",
     "glm53_sparse_mla_workspace_bytes",
     "glm53_sparse_mla",
+    "glm53_sparse_mla_noalloc",
     "glm53_convert_req_index",
     "glm53_sparse_mla_paged",
     "glm53_expand_pools",
@@ -61,6 +62,9 @@ def load():
     L.glm53_sparse_mla.restype = I
     L.glm53_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, I64, P, I64,
                                    P, I64, I64, P]
+    L.glm53_sparse_mla_noalloc.restype = I
+    L.glm53_sparse_mla_noalloc.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, I64,
+                                           P, I64, I64, P]
     L.glm53_convert_req_index.restype = I
     L.glm53_convert_req_index.argtypes = [P, P, I64, I64, I64, P, I64, P, I64, I64, I64, I64, I64, P]
     L.glm53_sparse_mla_paged.restype = I

@@ -34,6 +34,8 @@
 //     per 16x32 operand).  O^T accumulates in 8 MFMA tiles per wave.
 #include "glm53_common.h"
 
+#include <atomic>
+
 namespace glm53 {
 namespace {
 
@@ -837,6 +839,60 @@ int check_paged(const int32_t* req_id, const int32_t* block_table, int64_t num_r
 }  // namespace
 }  // namespace glm53
 
+namespace glm53 {
+namespace {
+
+// Static device scratch of glm53_sparse_mla_noalloc: the split partials of
+// at most GLM53_NOALLOC_MAX_PARTIAL_ROWS (token, split, head) rows, laid out
+// as the workspace of glm53_sparse_mla (part [rows][512], then lse [rows]).
+// Every GPU the library runs on holds its own copy until the process ends.
+static __device__ __align__(256) float scratch[GLM53_NOALLOC_MAX_PARTIAL_ROWS * (kLatent + 1)];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_ptr[kMaxDevices];   // device address of `scratch`, per device
+
+// The device address of the current device's `scratch`, looked up once per
+// device (the array's host-side name is not a device address).
+int device_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return GLM53_ERR_BAD_SHAPE;
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return static_cast<int>(hipErrorInvalidSymbol);
+    scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return 0;
+}
+
+}  // namespace
+}  // namespace glm53
+
+extern "C" int glm53_sparse_mla_noalloc(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
+                                        int64_t skv_t, int64_t seq_kv, const int32_t* indices,
+                                        int64_t si_t, int64_t num_tokens, int64_t num_heads,
+                                        int64_t topk, double sm_scale, int64_t num_splits, void* out,
+                                        int64_t so_t, int64_t so_h, void* stream) {
+  MlaArgs a;
+  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, indices, si_t, num_tokens, num_heads, topk,
+                   sm_scale, num_splits);
+  if (rc) return rc;
+  if (num_tokens == 0) return 0;
+  if (num_splits > 1 && partial_rows(num_tokens, num_heads, num_splits) > GLM53_NOALLOC_MAX_PARTIAL_ROWS)
+    return GLM53_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  if (num_splits > 1) {
+    rc = device_scratch(&ws);
+    if (rc) return rc;
+  }
+  const int64_t ws_bytes = num_splits > 1 ? glm53_sparse_mla_workspace_bytes(num_tokens, num_heads, num_splits) : 0;
+  return run_attention(a, num_tokens, num_heads, num_splits, ws, ws_bytes, out, so_t, so_h, stream);
+}
+
 extern "C" int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
                                 int64_t skv_t, int64_t seq_kv, const int32_t* indices,
                                 int64_t si_t, int64_t num_tokens, int64_t num_heads, int64_t topk,
@@ -1031,6 +1087,9 @@ extern "C" const char* glm53_error_string(int code) {
     case GLM53_ERR_MISALIGNED: return "pointer or stride not aligned as required";
     case GLM53_ERR_WORKSPACE: return "workspace missing or too small";
     case GLM53_ERR_BAD_DTYPE: return "unsupported dtype";
+    case GLM53_ERR_SCRATCH_LIMIT:
+      return "split partials exceed the static scratch of glm53_sparse_mla_noalloc "
+             "(GLM53_NOALLOC_MAX_PARTIAL_ROWS rows of tokens x splits x heads rounded up to 16)";
     default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }
 }

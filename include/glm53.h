@@ -27,6 +27,7 @@ extern "C" {
 #define GLM53_ERR_MISALIGNED     (-3)
 #define GLM53_ERR_WORKSPACE      (-4)
 #define GLM53_ERR_BAD_DTYPE      (-5)
+#define GLM53_ERR_SCRATCH_LIMIT  (-6)   /* beyond glm53_sparse_mla_noalloc's static scratch */
 
 int glm53_abi_version(void);
 const char* glm53_error_string(int code);
@@ -86,6 +87,28 @@ int glm53_sparse_mla(const void* q, int64_t sq_t, int64_t sq_h,
                      void* workspace, int64_t workspace_bytes,
                      void* out, int64_t so_t, int64_t so_h,
                      void* stream);
+
+/*
+ * glm53_sparse_mla without a workspace argument and without any allocation:
+ * the split partials go to a static device array of the library (one per
+ * GPU, held until the process ends), so the call suits callers that cannot
+ * allocate device memory (code under HIP graph capture that must not call
+ * hipMalloc, tight serving loops, harnesses that forbid allocation).  No
+ * counterpart in the reference.  Same arguments, kernels and output as
+ * glm53_sparse_mla; limit: num_tokens * num_splits * (num_heads rounded up
+ * to 16) <= GLM53_NOALLOC_MAX_PARTIAL_ROWS when num_splits > 1, else
+ * GLM53_ERR_SCRATCH_LIMIT (nothing launched).  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams) race.
+ * Nothing in it needs clearing: a call writes every partial row it reads.
+ */
+#define GLM53_NOALLOC_MAX_PARTIAL_ROWS 8192
+int glm53_sparse_mla_noalloc(const void* q, int64_t sq_t, int64_t sq_h,
+                             const void* kv, int64_t skv_t, int64_t seq_kv,
+                             const int32_t* indices, int64_t si_t,
+                             int64_t num_tokens, int64_t num_heads, int64_t topk,
+                             double sm_scale, int64_t num_splits,
+                             void* out, int64_t so_t, int64_t so_h,
+                             void* stream);
 
 /*
  * Request-relative indices.  The reference's vLLM adapter converts the
