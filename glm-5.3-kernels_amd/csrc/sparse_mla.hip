@@ -544,6 +544,251 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- long splits: waves in pairs
+// Splits of more than one chunk of flat-row indices (the prefill-shaped call:
+// one split of 2176 keys per token) take this kernel.  One workgroup of two
+// waves per (split, token, 16-head group) runs a single online-softmax stream
+// over the split's 32-key tiles in order -- the loop structure of
+// _sparse_mla_compute_tile with BLOCK_N = 32 -- and the two waves split the
+// latent: wave w gathers, converts and multiplies latents [256 w, 256 w + 256)
+// of every key.
+//   * S^T = K Q^T per 16-key half on v_mfma_f32_16x16x32_bf16 over the wave's
+//     256 latents (8 K-steps); the two waves' partial S^T meet in LDS (one
+//     two-wave barrier per tile) and both add them in the same order, so both
+//     run the same softmax on the same scores.  Row scales come from the lane
+//     that gathered the key (ds_bpermute).
+//   * O^T += V^T P^T for the wave's 16 latent tiles; V^T from the wave's bf16
+//     rows in LDS through ds_read_b64_tr_b16.  Rows are 544 bytes (8 banks
+//     apart) and rows 8-15 of every 16 swap the 16-byte halves of each
+//     32-byte block, so both the 16 rows of one write instruction and the 4
+//     rows of each transposing read land on distinct banks, while every
+//     address stays a per-lane base plus a constant (no per-tile address
+//     registers).
+//   * The partial S^T buffer is single: a second two-wave barrier before a
+//     wave overwrites its half keeps it from racing the other wave's read.
+//   * Gathers run two tiles ahead and index loads four; no barrier waits for
+//     them (a workgroup barrier here waits only for LDS traffic).
+//   * 38 KB of LDS and at most 256 registers per wave: four workgroups (eight
+//     waves) per CU.
+constexpr int kPairThreads = 128;
+constexpr int kHalfLat = kLatent / 2;
+constexpr int kPairVStride = kHalfLat + 16;   // bf16 per LDS V row: 544 bytes
+
+struct __attribute__((aligned(16))) PairShared {
+  uint16_t vbuf[2][kTile][kPairVStride];      // per wave: bf16 V half-rows of the tile
+  float4 red[2][2][64];                       // [wave][key half][lane]: partial S^T
+};
+
+constexpr int kPairRowBytes = kPairVStride * 2;
+
+// Byte offset of bf16 element (row, col) of a wave's V buffer: 16-byte chunk
+// (col / 8) ^ (row / 8 % 2) of the row.
+__device__ __forceinline__ int pair_vofs(int row, int col) {
+  return row * kPairRowBytes + 16 * ((col >> 3) ^ ((row >> 3) & 1)) + 2 * (col & 7);
+}
+
+template <int kMode>
+__global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void sparse_mla_pair_kernel(const MlaArgs a) {
+  static_assert(kMode == kFlatRows, "the pair kernel reads flat cache rows");
+  __shared__ PairShared sh;
+  const int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
+  const int w = uniform(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int start = split * a.split_len;
+  const int end = min(start + a.split_len, a.topk);
+  const int ntiles = end > start ? (end - start + kTile - 1) / kTile : 0;
+  const int head = hg * kHeads + c;
+  const bool head_ok = head < a.num_heads;
+  const int32_t* idx_t = a.idx + t * a.si_t;
+  uint8_t* vb = reinterpret_cast<uint8_t*>(&sh.vbuf[w][0][0]);
+  // per-lane LDS bases (pair_vofs of the lane's first element)
+  const int wr_lo = pair_vofs(c, 16 * g);        // row c, columns 16 g + [0, 8)
+  const int wr_hi = pair_vofs(c, 16 * g + 8);    //        columns 16 g + 8 + [0, 8)
+  const int tr_base = pair_vofs(4 * g + (c >> 2), 4 * (c & 3));
+
+  // Q^T fragments (B operand): head c, K-step (i, j) = latents
+  // 256 w + 64 i + 16 g + 8 j + [0, 8) -- the latents of the lane's gathered
+  // chunk 4 i + g of each key.
+  bf16x8 qf[4][2];
+  {
+    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + head * a.sq_h + kHalfLat * w);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+        qf[i][j] = __builtin_bit_cast(bf16x8, head_ok ? qp[8 * i + 2 * g + j] : make_uint4(0, 0, 0, 0));
+  }
+
+  f32x4 acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegLarge, l_run = 0.f;
+  bool acc_zero = true;
+
+  // Lane l < 32 loads the index of key l of tile n, from a clamped address
+  // (no branch); issue_rows masks positions past the split.  (Masking here
+  // would make the wave wait for the load, and with it for every gather
+  // issued before it.)
+  auto load_idx = [&](int n) { return idx_t[min(start + n * kTile + (lane & 31), end - 1)]; };
+  struct Rows {
+    uint4 d[2][4];      // [key half][chunk i]: latents 256 w + 64 i + 16 g + [0, 16) of key 16 u + c
+    float sv;           // lane l < 32: scale of key l (garbage for a masked key)
+    uint32_t vmask;     // bit l: key l valid
+  };
+  // Every load is unconditional: a masked key reads row 0 (its scores are
+  // replaced by -1e30, its weight by 0 and its scale by 0, and int8 codes
+  // are finite).  A branch around the loads would make the compiler's wait
+  // before the next use count no load as outstanding -- every tile would
+  // wait for the gathers still in flight.
+  auto issue_rows = [&](Rows& r, int raw, int n) {
+    const int pos = start + n * kTile + (lane & 31);
+    const int v = pos < end && raw >= 0 && static_cast<int64_t>(raw) < a.seq_kv ? raw : -1;
+    // the scale first: older than the rows, its wait comes free with theirs
+    r.sv = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(max(v, 0)) * a.skv + kLatent);
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int kid = max(__shfl(v, 16 * u + c, 64), 0);
+      const uint4* rp = reinterpret_cast<const uint4*>(a.kv + static_cast<int64_t>(kid) * a.skv + kHalfLat * w);
+#pragma unroll
+      for (int i = 0; i < 4; i++) r.d[u][i] = rp[4 * i + g];
+    }
+    r.vmask = static_cast<uint32_t>(__ballot(lane < kTile && v >= 0));
+  };
+
+  // One tile: convert + S^T + V to LDS, then the next-but-one tile's gathers,
+  // then the exchange, softmax and PV.
+  auto tile = [&](int n, Rows& cur, int& idx_ahead) {
+    f32x4 s_part[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        bf16x8 lo, hi;
+        i8x16_to_bf16(cur.d[u][i], lo, hi);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, qf[i][0], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, qf[i][1], sacc, 0, 0, 0);
+        // row 16 u + c, columns 64 i + 16 g + [0, 16): pair_vofs as base + constant
+        *reinterpret_cast<uint4*>(vb + wr_lo + u * 16 * kPairRowBytes + 128 * i) = __builtin_bit_cast(uint4, lo);
+        *reinterpret_cast<uint4*>(vb + wr_hi + u * 16 * kPairRowBytes + 128 * i) = __builtin_bit_cast(uint4, hi);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      s_part[u] = sacc;
+    }
+    __syncthreads();   // the other wave has read this wave's previous partial
+    sh.red[w][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
+    sh.red[w][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
+    // scales of the lane's keys 16 u + 4 g + r, and the validity bits
+    float sc[8];
+    const uint32_t kv_ok = ((cur.vmask >> (4 * g)) & 0xfu) | (((cur.vmask >> (16 + 4 * g)) & 0xfu) << 4);
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float v = __shfl(cur.sv, 16 * u + 4 * g + r, 64);
+        sc[4 * u + r] = (kv_ok >> (4 * u + r)) & 1 ? v : 0.f;
+      }
+    // the registers of this tile are free: gathers of tile n + 2, index of tile n + 4
+    // (kept below the conversions: hoisted above them the loads would hold a
+    // second tile's registers while the converted operands are still live)
+    __builtin_amdgcn_sched_barrier(0);
+    issue_rows(cur, idx_ahead, n + 2);
+    idx_ahead = load_idx(n + 4);
+    __syncthreads();
+
+    // Full scores: wave 0's partial + wave 1's, the same order in both waves.
+    float s[8];
+    {
+      const float4 p00 = sh.red[0][0][lane], p01 = sh.red[0][1][lane];
+      const float4 p10 = sh.red[1][0][lane], p11 = sh.red[1][1][lane];
+      const float4 h0[2] = {p00, p01}, h1[2] = {p10, p11};
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        float v = f4_get(h0[j >> 2], j & 3) + f4_get(h1[j >> 2], j & 3);
+        v *= sc[j];
+        v *= a.scale_log2;
+        s[j] = (kv_ok >> j) & 1 ? v : kNegLarge;
+      }
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    mx = rows_max(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    float pr[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) pr[j] = (kv_ok >> j) & 1 ? fast_exp2(s[j] - m_new) : 0.f;
+    float psum = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+    psum = rows_sum(psum);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+    // P^T operand: k-slot 8 g + j <-> key 16 (j / 4) + 4 g + j % 4.
+    const uint4 pw = make_uint4(pack_bf16x2(pr[0] * sc[0], pr[1] * sc[1]), pack_bf16x2(pr[2] * sc[2], pr[3] * sc[3]),
+                                pack_bf16x2(pr[4] * sc[4], pr[5] * sc[5]), pack_bf16x2(pr[6] * sc[6], pr[7] * sc[7]));
+    const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
+    if (!acc_zero && __ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < 16; dt++) {
+        acc[dt][0] *= alpha; acc[dt][1] *= alpha; acc[dt][2] *= alpha; acc[dt][3] *= alpha;
+      }
+    }
+    // ds_read_b64_tr_b16: in each 16-lane group, lane 4 r + q addresses row r,
+    // columns [4 q, 4 q + 4); lane c receives column c of the 4 rows.
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) {
+      // groups of 4 tiles: the reads of a group are not hoisted above the
+      // previous group's products (registers)
+      if (dt % 4 == 0 && dt > 0) __builtin_amdgcn_sched_barrier(0);
+      // rows 4 g + c / 4 and 16 + 4 g + c / 4, columns 16 dt + 4 (c % 4) + [0, 4)
+      const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(GLM53_LDS(i16x4, vb + tr_base + 32 * dt));
+      const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          GLM53_LDS(i16x4, vb + tr_base + 16 * kPairRowBytes + 32 * dt));
+      const i32x2 v0i = __builtin_bit_cast(i32x2, v0);
+      const i32x2 v1i = __builtin_bit_cast(i32x2, v1);
+      const uint4 vv = make_uint4(v0i[0], v0i[1], v1i[0], v1i[1]);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, acc[dt], 0, 0, 0);
+    }
+    acc_zero = false;
+  };
+
+  Rows ra, rb;
+  int ia = -1, ib = -1;   // index of tile n + 2 (n even: ia, odd: ib), then n + 4 after use
+  if (ntiles > 0) {
+    const int i0 = load_idx(0), i1 = load_idx(1);
+    ia = load_idx(2);
+    ib = load_idx(3);
+    issue_rows(ra, i0, 0);
+    issue_rows(rb, i1, 1);
+  }
+  // Tiles go in pairs (an odd count ends with a fully masked tile, which
+  // changes nothing): no branch in the loop body.
+  for (int n = 0; n < ntiles; n += 2) {
+    tile(n, ra, ia);
+    tile(n + 1, rb, ib);
+  }
+
+  // Epilogue: both waves hold the same m and l; each writes its latent half.
+  const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
+  if (!head_ok) return;
+  if (a.num_splits == 1 && !a.partials_only) {
+    uint16_t* op = a.out + t * a.so_t + head * a.so_h + kHalfLat * w + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++)
+      *reinterpret_cast<uint2*>(op + 16 * dt) = make_uint2(pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l),
+                                                           pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l));
+  } else {
+    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
+    float* pp = a.part + row * kLatent + kHalfLat * w + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++)
+      *reinterpret_cast<float4*>(pp + 16 * dt) = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l,
+                                                             acc[dt][2] * inv_l, acc[dt][3] * inv_l);
+    if (w == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
+  }
+}
+
 // Standalone conversion (the vLLM helper the reference's adapter calls):
 // out[t][k] = to_flat_row(block_table[req_id[t]], ..., indices[t][k]).
 __global__ __launch_bounds__(256) void convert_req_index_kernel(const int32_t* __restrict__ req_id,
@@ -766,6 +1011,8 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
     if (pipe) GLM53_LAUNCH(kPooledPos, true); else GLM53_LAUNCH(kPooledPos, false);
   } else if (mode == kPagedPos) {
     if (pipe) GLM53_LAUNCH(kPagedPos, true); else GLM53_LAUNCH(kPagedPos, false);
+  } else if (pipe && a.seq_kv > 0) {   // (its masked keys read row 0)
+    hipLaunchKernelGGL((sparse_mla_pair_kernel<kFlatRows>), grid, dim3(kPairThreads), 0, st, a);
   } else {
     if (pipe) GLM53_LAUNCH(kFlatRows, true); else GLM53_LAUNCH(kFlatRows, false);
   }
