@@ -113,6 +113,17 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
     from titan_kv import store_int8
     from titan_mla import triton_mla_sparse_attention, sparse_mla_partials, _choose_num_kv_splits_mi355x
     K, unroll = args.steps, args.unroll
+    caches = [kv8]
+    for li in range(1, max(1, args.rotate)):
+        _, xr, cr, sr = W.decode_cache(dev, seed=W.SEED_BENCH + 300 + li, dist="t3")
+        store_int8(xr, cr, sr)
+        del xr
+        caches.append(cr.view(n_rows, 1, W.ROW_BYTES))
+    turn = [0]
+
+    def next_cache():
+        turn[0] += 1
+        return caches[(turn[0] - 1) % len(caches)]
     if args.case == "writer_scattered":
         # the prefill-shaped call's write: 2048 rows -> randperm slots of a 262144-row cache
         _, _, new_rows, slots = W.prefill_inputs(dev, g8)
@@ -120,7 +131,7 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
         nbytes = W.writer_bytes(new_rows.shape[0])
     elif args.case == "prefill":
         qp, idxp, _, _ = W.prefill_inputs(dev, g8)
-        fn = lambda: triton_mla_sparse_attention(qp, kv8, idxp, W.SM_SCALE, num_kv_splits=args.splits)
+        fn = lambda: triton_mla_sparse_attention(qp, next_cache(), idxp, W.SM_SCALE, num_kv_splits=args.splits)
         nbytes = W.mla_bytes(idxp, n_rows)
     elif args.case == "decode_b1":
         g1, x1, cache1, slots1 = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
@@ -132,14 +143,16 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
         nbytes = W.mla_bytes(idx1, n_rows)
     else:   # decode_b8_split: the split kernel alone at the auto split count
         s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
-        fn = lambda: sparse_mla_partials(q8, kv8, idx8, W.SM_SCALE, s8)
+        fn = lambda: sparse_mla_partials(q8, next_cache(), idx8, W.SM_SCALE, s8)
         nbytes = W.mla_bytes(idx8, n_rows)
-    gr, _ = capture(torch, fn, unroll)
-    for _ in range(max(1, args.warmup // unroll)):
+    # one graph of `unroll` calls, each call reading the next cache of the rotation
+    per_graph = max(unroll, len(caches))
+    gr, _ = capture(torch, lambda: [fn() for _ in range(per_graph)], 1)
+    for _ in range(max(1, args.warmup // per_graph)):
         gr.replay()
-    us = timer.median_loop(gr, max(1, K // unroll)) / unroll
+    us = timer.median_loop(gr, max(1, K // per_graph)) / per_graph
     log(f"case {args.case}: {us:.3f} us per call, {nbytes / (us * 1e-6) / 1e9:.1f} GB/s algorithmic "
-        f"({nbytes} B), {K} calls, {unroll} per graph")
+        f"({nbytes} B), {K} calls, {per_graph} per graph, {len(caches)} cache(s)")
 
 
 def main():
@@ -148,6 +161,9 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only: skip extras and CPU baseline")
+    ap.add_argument("--rotate", type=int, default=1,
+                    help="with --case prefill / decode_b8_split: cycle the calls over this many 262144-row "
+                         "caches (HBM-resident when their total exceeds the 256 MB MALL)")
     ap.add_argument("--case", choices=("writer_scattered", "prefill", "decode_b1", "decode_b8_split"),
                     default=None,
                     help="time one workload alone (K calls, one per graph replay unless --unroll), print "
@@ -535,10 +551,10 @@ def main():
         # resident); rotation: consecutive calls over 3 caches (415 MB, read
         # from HBM).
         qp, idxp, new_rows, pslots = W.prefill_inputs(dev, g8)
-        pg, _ = capture(torch, lambda: triton_mla_sparse_attention(qp, kv8, idxp, W.SM_SCALE))
+        pg, _ = capture(torch, lambda: triton_mla_sparse_attention(qp, kv8, idxp, W.SM_SCALE), 3)
         pg.replay()
         log("prefill T=2048")
-        us_p = timer.median_loop(pg, 5)
+        us_p = timer.median_loop(pg, 3) / 3
         del pg
         pgr, _ = capture(torch, lambda: [triton_mla_sparse_attention(qp, c, idxp, W.SM_SCALE) for c in rot[:3]])
         pgr.replay()
