@@ -296,6 +296,18 @@ def main():
         pg.replay()
     us8_kernel_warm = timer.median_loop(pg, K // args.unroll, n_samples) / args.unroll
     del pg
+    # the floor under the step: the split kernel's memory chain alone (same
+    # grid, index loads, row gathers, partial stores; no arithmetic) + the merge
+    from titan_mla import sparse_mla_gather_floor, sparse_mla_merge
+    floor_step = lambda kv: sparse_mla_merge(sparse_mla_gather_floor(q8, kv, idx8, s8), 8, 16, s8)
+    fgr, _ = capture(torch, rotation(floor_step), 1)
+    fgk, _ = capture(torch, rotation(lambda kv: sparse_mla_gather_floor(q8, kv, idx8, s8)), 1)
+    for _ in range(max(1, Wm // args.unroll)):
+        fgr.replay()
+        fgk.replay()
+    us8_floor_step = timer.median_loop(fgr, K // args.unroll, n_samples) / args.unroll
+    us8_floor_kernel = timer.median_loop(fgk, K // args.unroll, n_samples) / args.unroll
+    del fgr, fgk
     g8_1, _ = capture(torch, mla_b8, 1)
     us8_cold = timer.cold_loop(g8_1, min(K, 50), flush)
     us8_single = timer.median_loop(g8_1, min(K, 100), n_samples)
@@ -305,6 +317,8 @@ def main():
                           "us_per_step_one_call_per_graph": round(us8_single, 3),
                           "us_split_kernel_alone_layer_rotation": round(us8_kernel, 3),
                           "us_split_kernel_alone_warm": round(us8_kernel_warm, 3),
+                          "us_floor_step_layer_rotation": round(us8_floor_step, 3),
+                          "us_floor_split_kernel_layer_rotation": round(us8_floor_kernel, 3),
                           "algorithmic_bytes": bytes8, "gbs_layer_rotation": round(gbs8, 1),
                           "gbs_warm": round(bytes8 / (us8_warm * 1e-6) / 1e9, 1),
                           "gbs_cold": round(bytes8 / (us8_cold * 1e-6) / 1e9, 1), "num_kv_splits": s8,
@@ -383,7 +397,15 @@ def main():
         us_r = timer.median_loop(grr, max(1, K // args.unroll)) / args.unroll
         extra["decode_b1"]["us_per_step_layer_rotation"] = round(us_r, 3)
         extra["decode_b1"]["gbs_layer_rotation"] = round(bytes1 / (us_r * 1e-6) / 1e9, 1)
-        del grr, rot1
+        # B=1's floor: its split kernel's memory chain + the merge, same rotation
+        from titan_mla import sparse_mla_gather_floor, sparse_mla_merge
+        fg1, _ = capture(torch, lambda: [sparse_mla_merge(sparse_mla_gather_floor(q1, rot1[i % len(rot1)], idx1, s1),
+                                                          1, 16, s1) for i in range(args.unroll)], 1)
+        for _ in range(3):
+            fg1.replay()
+        extra["decode_b1"]["us_floor_step_layer_rotation"] = round(
+            timer.median_loop(fg1, max(1, K // args.unroll)) / args.unroll, 3)
+        del grr, rot1, fg1
 
         # ------------------------------------------------------------ paged decode B=8
         # Request-relative indices: vLLM-style conversion + attention (two

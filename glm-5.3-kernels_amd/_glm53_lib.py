@@ -26,6 +26,7 @@ EXPORTED = (
     "glm53_sparse_mla_partials_bytes",
     "glm53_sparse_mla_partials",
     "glm53_sparse_mla_merge",
+    "glm53_sparse_mla_gather_floor",
     "glm53_moe_align_small",
     "glm53_moe_w4a16_repack",
     "glm53_moe_w4a16_gate_up",
@@ -82,6 +83,8 @@ def load():
                                             I64, P]
     L.glm53_sparse_mla_merge.restype = I
     L.glm53_sparse_mla_merge.argtypes = [P, I64, I64, I64, I64, P, I64, I64, P]
+    L.glm53_sparse_mla_gather_floor.restype = I
+    L.glm53_sparse_mla_gather_floor.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, I64, P, I64, P]
     L.glm53_moe_align_small.restype = I
     L.glm53_moe_align_small.argtypes = [P, I, I64, P, P, P, P]
     F = ctypes.c_float

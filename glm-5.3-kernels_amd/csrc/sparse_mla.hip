@@ -544,19 +544,22 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   }
 }
 
-// ---------------------------------------------------------------- long splits: waves in pairs
-// Splits of more than one chunk of flat-row indices (the prefill-shaped call:
-// one split of 2176 keys per token) take this kernel.  One workgroup of two
-// waves per (split, token, 16-head group) runs a single online-softmax stream
-// over the split's 32-key tiles in order -- the loop structure of
-// _sparse_mla_compute_tile with BLOCK_N = 32 -- and the two waves split the
-// latent: wave w gathers, converts and multiplies latents [256 w, 256 w + 256)
-// of every key.
+// ---------------------------------------------------------------- waves in pairs
+// A pair of waves runs one online-softmax stream over 32-key tiles -- the
+// loop structure of _sparse_mla_compute_tile with BLOCK_N = 32 -- and the two
+// waves split the latent: wave w of the pair gathers, converts and multiplies
+// latents [256 w, 256 w + 256) of every key.  A workgroup holds kPairs pairs
+// of one (split, token, 16-head group); the split's tiles are dealt to the
+// pairs in turn (tile n -> pair n % kPairs), and the pairs' streams meet in
+// LDS at the end (base-2 rescale to the largest max, summed in pair order).
+// kPairs = 1 is the reference's single stream per split (long splits: the
+// prefill-shaped call); more pairs put the tiles of a short decode split
+// into one round.
 //   * S^T = K Q^T per 16-key half on v_mfma_f32_16x16x32_bf16 over the wave's
 //     256 latents (8 K-steps); the two waves' partial S^T meet in LDS (one
-//     two-wave barrier per tile) and both add them in the same order, so both
-//     run the same softmax on the same scores.  Row scales come from the lane
-//     that gathered the key (ds_bpermute).
+//     barrier per tile) and both add them in the same order, so both run the
+//     same softmax on the same scores.  Row scales come from the lane that
+//     gathered the key (ds_bpermute).
 //   * O^T += V^T P^T for the wave's 16 latent tiles; V^T from the wave's bf16
 //     rows in LDS through ds_read_b64_tr_b16.  Rows are 544 bytes (8 banks
 //     apart) and rows 8-15 of every 16 swap the 16-byte halves of each
@@ -564,22 +567,30 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 //     rows of each transposing read land on distinct banks, while every
 //     address stays a per-lane base plus a constant (no per-tile address
 //     registers).
-//   * The partial S^T buffer is single: a second two-wave barrier before a
-//     wave overwrites its half keeps it from racing the other wave's read.
-//   * Gathers run two tiles ahead and index loads four; no barrier waits for
-//     them (a workgroup barrier here waits only for LDS traffic).
-//   * 38 KB of LDS and at most 256 registers per wave: four workgroups (eight
-//     waves) per CU.
-constexpr int kPairThreads = 128;
+//   * The partial S^T buffer is single: a second barrier before a wave
+//     overwrites its half keeps it from racing the other wave's read.
+//   * Gathers run kRing tiles ahead and index loads 2 kRing; no barrier waits
+//     for them (a workgroup barrier here waits only for LDS traffic).  Every
+//     load is unconditional: a masked key reads row 0 (its score becomes
+//     -1e30, its weight and scale 0, and int8 codes are finite); a branch
+//     around the loads would make the compiler's wait before the next use
+//     count no load as outstanding, draining the prefetch every tile.
+//   * 38 KB of LDS per pair.
 constexpr int kHalfLat = kLatent / 2;
 constexpr int kPairVStride = kHalfLat + 16;   // bf16 per LDS V row: 544 bytes
-
-struct __attribute__((aligned(16))) PairShared {
-  uint16_t vbuf[2][kTile][kPairVStride];      // per wave: bf16 V half-rows of the tile
-  float4 red[2][2][64];                       // [wave][key half][lane]: partial S^T
-};
-
 constexpr int kPairRowBytes = kPairVStride * 2;
+
+template <int kPairs>
+struct __attribute__((aligned(16))) PairShared {
+  union {
+    uint16_t vbuf[2 * kPairs][kTile][kPairVStride];   // per wave: bf16 V half-rows of the tile
+    struct {
+      float rows[kPairs][kHeads][kRowStride];         // each pair's acc, row-major
+      float ml[kPairs][kHeads][2];                    // each pair's (m, l) per head
+    } fin;
+  };
+  float4 red[kPairs][2][2][64];                       // [pair][wave][key half][lane]: partial S^T
+};
 
 // Byte offset of bf16 element (row, col) of a wave's V buffer: 16-byte chunk
 // (col / 8) ^ (row / 8 % 2) of the row.
@@ -587,23 +598,36 @@ __device__ __forceinline__ int pair_vofs(int row, int col) {
   return row * kPairRowBytes + 16 * ((col >> 3) ^ ((row >> 3) & 1)) + 2 * (col & 7);
 }
 
-template <int kMode>
-__global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <int kMode, int kPairs, int kRing>
+__global__ __launch_bounds__(128 * kPairs) __attribute__((amdgpu_waves_per_eu(kPairs == 1 ? 1 : 2, kPairs == 1 ? 1 : 2)))
 void sparse_mla_pair_kernel(const MlaArgs a) {
   static_assert(kMode == kFlatRows, "the pair kernel reads flat cache rows");
-  __shared__ PairShared sh;
-  const int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
-  const int w = uniform(threadIdx.x >> 6);
+  static_assert(kRing == 1 || kRing == 2, "one or two tiles of gathers ahead");
+  __shared__ PairShared<kPairs> sh;
+  int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
+  if (kPairs > 1 && (gridDim.y * gridDim.z) % 8 == 0) {
+    // all splits of a (token, head group) unit on one XCD, where the merge
+    // kernel reads them back (see sparse_mla_kernel)
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int units = gridDim.y * gridDim.z;
+    split = lin / units;
+    t = (lin % units) % gridDim.y;
+    hg = (lin % units) / gridDim.y;
+  }
+  const int wv = uniform(threadIdx.x >> 6);
+  const int p = wv >> 1;          // pair
+  const int w = wv & 1;           // latent half of this wave
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   const int c = lane & 15;
   const int start = split * a.split_len;
   const int end = min(start + a.split_len, a.topk);
   const int ntiles = end > start ? (end - start + kTile - 1) / kTile : 0;
+  const int niter = (ntiles + kPairs - 1) / kPairs;   // tiles per pair, the same for every pair
   const int head = hg * kHeads + c;
   const bool head_ok = head < a.num_heads;
   const int32_t* idx_t = a.idx + t * a.si_t;
-  uint8_t* vb = reinterpret_cast<uint8_t*>(&sh.vbuf[w][0][0]);
+  uint8_t* vb = reinterpret_cast<uint8_t*>(&sh.vbuf[wv][0][0]);
   // per-lane LDS bases (pair_vofs of the lane's first element)
   const int wr_lo = pair_vofs(c, 16 * g);        // row c, columns 16 g + [0, 8)
   const int wr_hi = pair_vofs(c, 16 * g + 8);    //        columns 16 g + 8 + [0, 8)
@@ -628,23 +652,19 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
   float m_run = kNegLarge, l_run = 0.f;
   bool acc_zero = true;
 
-  // Lane l < 32 loads the index of key l of tile n, from a clamped address
-  // (no branch); issue_rows masks positions past the split.  (Masking here
-  // would make the wave wait for the load, and with it for every gather
-  // issued before it.)
-  auto load_idx = [&](int n) { return idx_t[min(start + n * kTile + (lane & 31), end - 1)]; };
+  // The pair's j-th tile is tile p + kPairs j of the split.  Lane l < 32
+  // loads the index of key l of it, from a clamped address (no branch);
+  // issue_rows masks positions past the split.  (Masking here would make the
+  // wave wait for the load, and with it for every gather issued before it.)
+  auto tile_pos = [&](int j) { return start + (p + kPairs * j) * kTile + (lane & 31); };
+  auto load_idx = [&](int j) { return idx_t[min(tile_pos(j), end - 1)]; };
   struct Rows {
     uint4 d[2][4];      // [key half][chunk i]: latents 256 w + 64 i + 16 g + [0, 16) of key 16 u + c
     float sv;           // lane l < 32: scale of key l (garbage for a masked key)
     uint32_t vmask;     // bit l: key l valid
   };
-  // Every load is unconditional: a masked key reads row 0 (its scores are
-  // replaced by -1e30, its weight by 0 and its scale by 0, and int8 codes
-  // are finite).  A branch around the loads would make the compiler's wait
-  // before the next use count no load as outstanding -- every tile would
-  // wait for the gathers still in flight.
-  auto issue_rows = [&](Rows& r, int raw, int n) {
-    const int pos = start + n * kTile + (lane & 31);
+  auto issue_rows = [&](Rows& r, int raw, int j) {
+    const int pos = tile_pos(j);
     const int v = pos < end && raw >= 0 && static_cast<int64_t>(raw) < a.seq_kv ? raw : -1;
     // the scale first: older than the rows, its wait comes free with theirs
     r.sv = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(max(v, 0)) * a.skv + kLatent);
@@ -658,9 +678,9 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
     r.vmask = static_cast<uint32_t>(__ballot(lane < kTile && v >= 0));
   };
 
-  // One tile: convert + S^T + V to LDS, then the next-but-one tile's gathers,
+  // One tile: convert + S^T + V to LDS, then the gathers kRing tiles on,
   // then the exchange, softmax and PV.
-  auto tile = [&](int n, Rows& cur, int& idx_ahead) {
+  auto tile = [&](int j, Rows& cur, int& idx_ahead) {
     f32x4 s_part[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -679,9 +699,9 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
       s_part[u] = sacc;
     }
     __syncthreads();   // the other wave has read this wave's previous partial
-    sh.red[w][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
-    sh.red[w][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
-    // scales of the lane's keys 16 u + 4 g + r, and the validity bits
+    sh.red[p][w][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
+    sh.red[p][w][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
+    // scales of the lane's keys 16 u + 4 g + r (0 for a masked key), and the validity bits
     float sc[8];
     const uint32_t kv_ok = ((cur.vmask >> (4 * g)) & 0xfu) | (((cur.vmask >> (16 + 4 * g)) & 0xfu) << 4);
 #pragma unroll
@@ -691,26 +711,26 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
         const float v = __shfl(cur.sv, 16 * u + 4 * g + r, 64);
         sc[4 * u + r] = (kv_ok >> (4 * u + r)) & 1 ? v : 0.f;
       }
-    // the registers of this tile are free: gathers of tile n + 2, index of tile n + 4
+    // the registers of this tile are free: gathers kRing tiles on, index 2 kRing on
     // (kept below the conversions: hoisted above them the loads would hold a
     // second tile's registers while the converted operands are still live)
     __builtin_amdgcn_sched_barrier(0);
-    issue_rows(cur, idx_ahead, n + 2);
-    idx_ahead = load_idx(n + 4);
+    issue_rows(cur, idx_ahead, j + kRing);
+    idx_ahead = load_idx(j + 2 * kRing);
     __syncthreads();
 
     // Full scores: wave 0's partial + wave 1's, the same order in both waves.
     float s[8];
     {
-      const float4 p00 = sh.red[0][0][lane], p01 = sh.red[0][1][lane];
-      const float4 p10 = sh.red[1][0][lane], p11 = sh.red[1][1][lane];
+      const float4 p00 = sh.red[p][0][0][lane], p01 = sh.red[p][0][1][lane];
+      const float4 p10 = sh.red[p][1][0][lane], p11 = sh.red[p][1][1][lane];
       const float4 h0[2] = {p00, p01}, h1[2] = {p10, p11};
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        float v = f4_get(h0[j >> 2], j & 3) + f4_get(h1[j >> 2], j & 3);
-        v *= sc[j];
+      for (int jj = 0; jj < 8; jj++) {
+        float v = f4_get(h0[jj >> 2], jj & 3) + f4_get(h1[jj >> 2], jj & 3);
+        v *= sc[jj];
         v *= a.scale_log2;
-        s[j] = (kv_ok >> j) & 1 ? v : kNegLarge;
+        s[jj] = (kv_ok >> jj) & 1 ? v : kNegLarge;
       }
     }
     float mx = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
@@ -719,12 +739,12 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
     const float alpha = fast_exp2(m_run - m_new);
     float pr[8];
 #pragma unroll
-    for (int j = 0; j < 8; j++) pr[j] = (kv_ok >> j) & 1 ? fast_exp2(s[j] - m_new) : 0.f;
+    for (int jj = 0; jj < 8; jj++) pr[jj] = (kv_ok >> jj) & 1 ? fast_exp2(s[jj] - m_new) : 0.f;
     float psum = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
     psum = rows_sum(psum);
     l_run = l_run * alpha + psum;
     m_run = m_new;
-    // P^T operand: k-slot 8 g + j <-> key 16 (j / 4) + 4 g + j % 4.
+    // P^T operand: k-slot 8 g + jj <-> key 16 (jj / 4) + 4 g + jj % 4.
     const uint4 pw = make_uint4(pack_bf16x2(pr[0] * sc[0], pr[1] * sc[1]), pack_bf16x2(pr[2] * sc[2], pr[3] * sc[3]),
                                 pack_bf16x2(pr[4] * sc[4], pr[5] * sc[5]), pack_bf16x2(pr[6] * sc[6], pr[7] * sc[7]));
     const bf16x8 pb = __builtin_bit_cast(bf16x8, pw);
@@ -753,39 +773,185 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
     acc_zero = false;
   };
 
-  Rows ra, rb;
-  int ia = -1, ib = -1;   // index of tile n + 2 (n even: ia, odd: ib), then n + 4 after use
-  if (ntiles > 0) {
-    const int i0 = load_idx(0), i1 = load_idx(1);
-    ia = load_idx(2);
-    ib = load_idx(3);
-    issue_rows(ra, i0, 0);
-    issue_rows(rb, i1, 1);
-  }
-  // Tiles go in pairs (an odd count ends with a fully masked tile, which
-  // changes nothing): no branch in the loop body.
-  for (int n = 0; n < ntiles; n += 2) {
-    tile(n, ra, ia);
-    tile(n + 1, rb, ib);
+  // Every pair runs niter tiles (a tile past the split is fully masked and
+  // changes nothing): the barriers of all waves match.  With two tiles of
+  // gathers ahead the tiles go in pairs -- no branch in the loop body.
+  if (kRing == 2) {
+    Rows ra, rb;
+    int ia = -1, ib = -1;   // index of tile j + 2 (j even: ia, odd: ib), then j + 4 after use
+    if (niter > 0) {
+      const int i0 = load_idx(0), i1 = load_idx(1);
+      ia = load_idx(2);
+      ib = load_idx(3);
+      issue_rows(ra, i0, 0);
+      issue_rows(rb, i1, 1);
+    }
+    for (int j = 0; j < niter; j += 2) {
+      tile(j, ra, ia);
+      tile(j + 1, rb, ib);
+    }
+  } else {
+    Rows ra;
+    int ia = -1;            // index of tile j + 1, then j + 2 after use
+    if (niter > 0) {
+      const int i0 = load_idx(0);
+      ia = load_idx(1);
+      issue_rows(ra, i0, 0);
+    }
+    for (int j = 0; j < niter; j++) tile(j, ra, ia);
   }
 
-  // Epilogue: both waves hold the same m and l; each writes its latent half.
-  const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
-  if (!head_ok) return;
-  if (a.num_splits == 1 && !a.partials_only) {
-    uint16_t* op = a.out + t * a.so_t + head * a.so_h + kHalfLat * w + 4 * g;
+  if (kPairs == 1) {
+    // Both waves hold the same m and l; each writes its latent half.
+    const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
+    if (!head_ok) return;
+    if (a.num_splits == 1 && !a.partials_only) {
+      uint16_t* op = a.out + t * a.so_t + head * a.so_h + kHalfLat * w + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 16; dt++)
+        *reinterpret_cast<uint2*>(op + 16 * dt) = make_uint2(pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l),
+                                                             pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l));
+    } else {
+      const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
+      float* pp = a.part + row * kLatent + kHalfLat * w + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 16; dt++)
+        *reinterpret_cast<float4*>(pp + 16 * dt) = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l,
+                                                               acc[dt][2] * inv_l, acc[dt][3] * inv_l);
+      if (w == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
+    }
+    return;
+  }
+
+  // kPairs > 1: the pairs park their accumulators row-major in LDS, then every
+  // wave finishes whole result rows (m = max over pairs, base-2 rescale,
+  // summed in pair order, 1 / l) with contiguous stores.
+  __syncthreads();   // V buffers are free
+  {
+    float* rp = &sh.fin.rows[p][c][kHalfLat * w + 4 * g];
 #pragma unroll
     for (int dt = 0; dt < 16; dt++)
-      *reinterpret_cast<uint2*>(op + 16 * dt) = make_uint2(pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l),
-                                                           pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l));
-  } else {
-    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
-    float* pp = a.part + row * kLatent + kHalfLat * w + 4 * g;
+      *reinterpret_cast<float4*>(rp + 16 * dt) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+    if (w == 0 && g == 0) {
+      sh.fin.ml[p][c][0] = m_run;
+      sh.fin.ml[p][c][1] = l_run;
+    }
+  }
+  __syncthreads();
+  constexpr int kRowsPerWave = kHeads / (2 * kPairs);
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++)
-      *reinterpret_cast<float4*>(pp + 16 * dt) = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l,
-                                                             acc[dt][2] * inv_l, acc[dt][3] * inv_l);
-    if (w == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
+  for (int k = 0; k < kRowsPerWave; k++) {
+    const int r = kRowsPerWave * wv + k;    // result row (head in the group), uniform per wave
+    const int hd = hg * kHeads + r;
+    if (hd >= a.num_heads) break;
+    float mm = kNegLarge;
+#pragma unroll
+    for (int q = 0; q < kPairs; q++) mm = fmaxf(mm, sh.fin.ml[q][r][0]);
+    float fs[kPairs];
+    float l = 0.f;
+#pragma unroll
+    for (int q = 0; q < kPairs; q++) {
+      fs[q] = fast_exp2(sh.fin.ml[q][r][0] - mm);
+      l += sh.fin.ml[q][r][1] * fs[q];
+    }
+    const float inv_l = 1.f / (l > 0.f ? l : 1.f);
+    auto fin4 = [&](int col) {
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int q = 0; q < kPairs; q++) {
+        const float4 x = *reinterpret_cast<const float4*>(&sh.fin.rows[q][r][col]);
+        o.x += x.x * fs[q]; o.y += x.y * fs[q]; o.z += x.z * fs[q]; o.w += x.w * fs[q];
+      }
+      return make_float4(o.x * inv_l, o.y * inv_l, o.z * inv_l, o.w * inv_l);
+    };
+    if (a.num_splits == 1 && !a.partials_only) {
+      const float4 u = fin4(8 * lane);
+      const float4 v = fin4(8 * lane + 4);
+      uint4 o;
+      o.x = pack_bf16x2(u.x, u.y);
+      o.y = pack_bf16x2(u.z, u.w);
+      o.z = pack_bf16x2(v.x, v.y);
+      o.w = pack_bf16x2(v.z, v.w);
+      uint16_t* op = a.out + t * a.so_t + hd * a.so_h + 8 * lane;
+      if (a.out_align16) {
+        *reinterpret_cast<uint4*>(op) = o;
+      } else {
+        reinterpret_cast<uint2*>(op)[0] = make_uint2(o.x, o.y);
+        reinterpret_cast<uint2*>(op)[1] = make_uint2(o.z, o.w);
+      }
+    } else {
+      const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + hd;
+      float* pp = a.part + row * kLatent;
+      *reinterpret_cast<float4*>(pp + 4 * lane) = fin4(4 * lane);
+      *reinterpret_cast<float4*>(pp + 256 + 4 * lane) = fin4(256 + 4 * lane);
+      if (lane == 0) a.lse[row] = (mm + log2f(l)) * kLn2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- gather floor (diagnostic)
+// The memory chain of sparse_mla_kernel's decode splits alone: the same grid
+// and workgroup shape, the same index loads, row gathers and scale loads per
+// lane, and the same partial-row and LSE stores, with no arithmetic between
+// them (the loaded bytes are folded with XOR so that no load is dead).  Its
+// duration is the floor that the split kernel's conversions, products and
+// softmax add to.
+__global__ __launch_bounds__(kThreads) void sparse_mla_gather_floor_kernel(const MlaArgs a) {
+  int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
+  if ((gridDim.y * gridDim.z) % 8 == 0) {
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int units = gridDim.y * gridDim.z;
+    split = lin / units;
+    t = (lin % units) % gridDim.y;
+    hg = (lin % units) / gridDim.y;
+  }
+  const int w = uniform(threadIdx.x >> 6);
+  const int sl = w & (kSlices - 1);
+  const int kg = w / kSlices;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int start = split * a.split_len;
+  const int end = min(start + a.split_len, a.topk);
+  const int32_t* idx_t = a.idx + t * a.si_t;
+  const int head = hg * kHeads + c;
+  uint32_t fold = 0;
+  if (head < a.num_heads) {
+    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + head * a.sq_h + kSlice * sl + 16 * g);
+    const uint4 q0 = qp[0], q1 = qp[1], q2 = qp[8], q3 = qp[9];
+    fold = q0.x ^ q1.y ^ q2.z ^ q3.w;
+  }
+  for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile) {
+#pragma unroll
+    for (int r = 0; r < kRounds; r++) {
+      const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
+      int v = pos < end ? idx_t[pos] : -1;
+      if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv) v = -1;
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int kid = __shfl(v, 16 * u + c, 64);
+        if (kid >= 0) {
+          const uint4* rp = reinterpret_cast<const uint4*>(a.kv + static_cast<int64_t>(kid) * a.skv + kSlice * sl + 16 * g);
+          const uint4 k0 = rp[0], k1 = rp[4];
+          fold ^= k0.x ^ k0.y ^ k0.z ^ k0.w ^ k1.x ^ k1.y ^ k1.z ^ k1.w;
+        }
+      }
+      if (sl == 0 && lane < kTile && v >= 0)
+        fold ^= *reinterpret_cast<const uint32_t*>(a.kv + static_cast<int64_t>(v) * a.skv + kLatent);
+    }
+  }
+  // a finite float from the folded bits, stored where the split kernel stores
+  const float x = static_cast<float>(fold & 0xffff);
+#pragma unroll
+  for (int k = 0; k < kHeads / kWaves; k++) {
+    const int r = (kHeads / kWaves) * w + k;
+    const int hd = hg * kHeads + r;
+    if (hd >= a.num_heads) break;
+    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + hd;
+    float* pp = a.part + row * kLatent;
+    *reinterpret_cast<float4*>(pp + 4 * lane) = make_float4(x, x, x, x);
+    *reinterpret_cast<float4*>(pp + 256 + 4 * lane) = make_float4(x, x, x, x);
+    if (lane == 0) a.lse[row] = x;
   }
 }
 
@@ -1012,7 +1178,7 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   } else if (mode == kPagedPos) {
     if (pipe) GLM53_LAUNCH(kPagedPos, true); else GLM53_LAUNCH(kPagedPos, false);
   } else if (pipe && a.seq_kv > 0) {   // (its masked keys read row 0)
-    hipLaunchKernelGGL((sparse_mla_pair_kernel<kFlatRows>), grid, dim3(kPairThreads), 0, st, a);
+    hipLaunchKernelGGL((sparse_mla_pair_kernel<kFlatRows, 1, 2>), grid, dim3(128), 0, st, a);
   } else {
     if (pipe) GLM53_LAUNCH(kFlatRows, true); else GLM53_LAUNCH(kFlatRows, false);
   }
@@ -1299,6 +1465,30 @@ extern "C" int glm53_sparse_mla_partials(const void* q, int64_t sq_t, int64_t sq
   a.partials_only = 1;
   (void)hipGetLastError();
   launch_attention(a, num_tokens, static_cast<hipStream_t>(stream));
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int glm53_sparse_mla_gather_floor(const void* q, int64_t sq_t, int64_t sq_h, const void* kv,
+                                             int64_t skv_t, int64_t seq_kv, const int32_t* indices,
+                                             int64_t si_t, int64_t num_tokens, int64_t num_heads,
+                                             int64_t topk, int64_t num_splits, void* partials,
+                                             int64_t partials_bytes, void* stream) {
+  MlaArgs a;
+  int rc = prepare(a, q, sq_t, sq_h, kv, skv_t, seq_kv, indices, si_t, num_tokens, num_heads, topk, 1.0,
+                   num_splits);
+  if (rc) return rc;
+  if (num_tokens == 0) return 0;
+  const int64_t need = glm53_sparse_mla_partials_bytes(num_tokens, num_heads, num_splits);
+  if (!partials || partials_bytes < need) return GLM53_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(partials) % 16) return GLM53_ERR_MISALIGNED;
+  if (a.split_len > kChunkTiles * kTile) return GLM53_ERR_BAD_SHAPE;   // decode splits only
+  const int64_t rows = partial_rows(num_tokens, num_heads, num_splits);
+  a.part = static_cast<float*>(partials);
+  a.lse = static_cast<float*>(partials) + rows * kLatent;
+  const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
+                  static_cast<unsigned>(a.heads_padded / kHeads));
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(sparse_mla_gather_floor_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -353,6 +353,27 @@ def sparse_mla_partials(q, kv, indices, sm_scale, num_kv_splits):
     return buf
 
 
+def sparse_mla_gather_floor(q, kv, indices, num_kv_splits, out=None):
+    """Diagnostic: the memory chain of sparse_mla_partials alone (the same
+    grid, index loads, row gathers and partial stores, no arithmetic; the
+    buffer then holds junk) -- the floor under the split kernel's time.
+    Decode splits only (at most 256 indices per split)."""
+    assert q.dim() == 3 and q.shape[2] == _BLOCK_DMODEL and q.dtype == torch.bfloat16 and q.is_contiguous()
+    assert kv.dtype == torch.int8 and kv.shape[1] == 1 and kv.shape[2] == _ROW_BYTES
+    assert indices.dtype == torch.int32 and indices.stride(2) == 1
+    T, H, _ = q.shape
+    L = _lib.load()
+    nbytes = L.glm53_sparse_mla_partials_bytes(T, H, num_kv_splits)
+    buf = out if out is not None else torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = L.glm53_sparse_mla_gather_floor(q.data_ptr(), q.stride(0), q.stride(1), kv.data_ptr(), kv.stride(0),
+                                             kv.shape[0], indices.data_ptr(), indices.stride(0), T, H,
+                                             indices.shape[2], num_kv_splits, buf.data_ptr(), nbytes,
+                                             _lib.stream_handle(q.device))
+    _lib.check(rc, "glm53_sparse_mla_gather_floor")
+    return buf
+
+
 def sparse_mla_merge(partials, num_tokens, num_heads, num_kv_splits):
     """Second stage: log-sum-exp merge of sparse_mla_partials' buffer."""
     out = torch.empty((num_tokens, num_heads, _BLOCK_DV), dtype=torch.bfloat16, device=partials.device)

@@ -215,6 +215,20 @@ int glm53_sparse_mla_partials(const void* q, int64_t sq_t, int64_t sq_h,
                               double sm_scale, int64_t num_splits,
                               void* partials, int64_t partials_bytes,
                               void* stream);
+/*
+ * Diagnostic, no counterpart in the reference: the memory chain of
+ * glm53_sparse_mla_partials alone for decode splits (at most 256 indices per
+ * split) -- the same grid, index loads, row gathers, scale loads and
+ * partial/LSE stores, with no arithmetic (the partials hold junk).  Its time
+ * is the floor that the split kernel's conversions, products and softmax
+ * add to; bench.py reports both.
+ */
+int glm53_sparse_mla_gather_floor(const void* q, int64_t sq_t, int64_t sq_h,
+                                  const void* kv, int64_t skv_t, int64_t seq_kv,
+                                  const int32_t* indices, int64_t si_t,
+                                  int64_t num_tokens, int64_t num_heads, int64_t topk,
+                                  int64_t num_splits, void* partials, int64_t partials_bytes,
+                                  void* stream);
 int glm53_sparse_mla_merge(const void* partials, int64_t partials_bytes,
                            int64_t num_tokens, int64_t num_heads,
                            int64_t num_splits, void* out, int64_t so_t,

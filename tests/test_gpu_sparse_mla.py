@@ -449,3 +449,24 @@ def test_merge_beyond_register_splits(cuda, oracle, small_cache):
         want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s, groups=GROUPS,
                                  block_n=BLOCK, lazy=LAZY, nthreads=oracle.default_threads())
         compare(out, want, ("merge loop path", s))
+
+
+def test_gather_floor_diagnostic(cuda, small_cache):
+    """The memory-chain probe runs on the decode grids, fills the partials
+    buffer the merge reads (junk, finite), and refuses splits longer than one
+    chunk of gathers."""
+    from titan_mla import sparse_mla_gather_floor, sparse_mla_merge
+    w, _ = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    g = W.gen(cuda, 21)
+    q = torch.randn(8, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+    idx = torch.randint(-8, n, (8, 1, 2176), generator=g, device=cuda, dtype=torch.int32)
+    for s in (17, 34):
+        log_case("gather floor", s)
+        buf = sparse_mla_gather_floor(q, kv, idx, s)
+        out = sparse_mla_merge(buf, 8, 16, s)
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(buf.view(torch.float32)).all()) and out.shape == (8, 16, 512)
+    with pytest.raises(RuntimeError):
+        sparse_mla_gather_floor(q, kv, idx, 1)
