@@ -568,6 +568,32 @@ def main():
             del sets, q_i, cache_i, w_i, lens_i, bt_i, logits_i
         extra["indexer_decode"] = idx
 
+        # ------------------------------------------------------------ sparse indexer (prefill shape)
+        # The reference's TP4 prefill indexer benchmark, replicated branch on
+        # one GPU (docs/measurements.json:3196-3201: 20.632 ms wall median for
+        # 2048 rows): 2048 query rows at the end of a 262144-token context,
+        # logits over the complete pools before each row (65536 pools) and the
+        # top 512 per row.  Three calls per graph, median of 5 samples.
+        gi = W.gen(dev, W.SEED_BENCH + 2048)
+        qpi, cpi, wpi, lpi, bpi, npi = W.indexer_prefill_inputs(dev, gi)
+        pre_fn = lambda: indexer_topk(fp8_paged_mqa_logits(qpi, cpi, wpi, lpi, bpi, npi, clean_logits=False), lpi,
+                                      W.INDEX_TOPK_POOLS)
+        gpi, _ = capture(torch, pre_fn, 3)
+        gpi.replay()
+        log("indexer prefill shape (2048 rows)")
+        us_pi = timer.median_loop(gpi, 2) / 3
+        del gpi
+        glo, _ = capture(torch, lambda: fp8_paged_mqa_logits(qpi, cpi, wpi, lpi, bpi, npi, clean_logits=False), 3)
+        glo.replay()
+        us_plo = timer.median_loop(glo, 2) / 3
+        del glo
+        extra["indexer_prefill_2048_rows"] = {"ms_logits_plus_topk": round(us_pi / 1e3, 4),
+                                              "ms_logits": round(us_plo / 1e3, 4),
+                                              "reference_ms_replicated_sm80": 20.632,
+                                              "speedup_vs_reference": round(20.632e3 / us_pi, 1),
+                                              "pools": npi, "rows": int(lpi.numel()), "heads": W.INDEX_HEADS}
+        del qpi, cpi, wpi, lpi, bpi
+
         # ------------------------------------------------------------ prefill-shaped
         # T=2048 tokens, one split.  warm: one cache replayed (138 MB, MALL-
         # resident); rotation: consecutive calls over 3 caches (415 MB, read

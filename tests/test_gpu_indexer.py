@@ -328,3 +328,26 @@ def test_decode_graph_replay(cuda, decode_b8):
         assert torch.equal(captured, eager), i
         fn()
         torch.cuda.synchronize()
+
+
+@pytest.mark.slow
+def test_prefill_shape_sampled_rows(cuda, oracle):
+    """The reference's prefill indexer shape: 2048 query rows of one request
+    at the end of a 262144-token context, each scoring the complete pools
+    before it (65024..65536 of 65536), then its top 512.  Logits of sampled
+    rows against the float64 oracle; the selection of every row bit-exact
+    against the oracle's selection on the same GPU logits."""
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits, indexer_topk
+    g = torch.Generator(device=cuda).manual_seed(2048)
+    q, cache, w, lens, bt, pools = W.indexer_prefill_inputs(cuda, g)
+    log_case("indexer prefill shape: 2048 rows x 65536 pools")
+    logits = fp8_paged_mqa_logits(q, cache, w, lens, bt, pools, clean_logits=False)
+    top = indexer_topk(logits, lens, 512)
+    torch.cuda.synchronize()
+    rows = [0, 1, 777, 2046, 2047]
+    sel = torch.as_tensor(rows, device=cuda)
+    check_logits(oracle, logits.index_select(0, sel), q.view(torch.uint8).index_select(0, sel), cache, w.index_select(0, sel),
+                 lens.index_select(0, sel), bt.index_select(0, sel), pools, clean=False)
+    want = oracle.indexer_topk(logits.cpu().numpy(), lens.cpu().numpy(), 512)
+    assert np.array_equal(top.cpu().numpy(), want)
