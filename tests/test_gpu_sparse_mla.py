@@ -470,3 +470,36 @@ def test_gather_floor_diagnostic(cuda, small_cache):
         assert bool(torch.isfinite(buf.view(torch.float32)).all()) and out.shape == (8, 16, 512)
     with pytest.raises(RuntimeError):
         sparse_mla_gather_floor(q, kv, idx, 1)
+
+
+def test_long_split_pair_kernel_edges(cuda, oracle, small_cache):
+    """Splits longer than one chunk (256 indices) run on the pair kernel (one
+    online-softmax stream per split): against the reference's single stream
+    (groups=1, BLOCK_N=32) with odd tile counts (352 = 11 tiles, 288 = 9), a
+    last split shorter than the others (1088 in 3 splits), split partials
+    merged (2176 in 2 splits, 20 heads: a padded head group), pads and
+    indices outside the cache both ways; all -1 gives exactly 0; an empty
+    cache (no rows) gives exactly 0 without reading it."""
+    from titan_mla import triton_mla_sparse_attention
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    g = W.gen(cuda, 99)
+    for T, H, topk, splits in ((5, 20, 2176, 2), (3, 16, 352, 1), (2, 16, 288, 1), (4, 32, 1088, 3),
+                               (3, 16, 2176, 1), (2, 16, 320, 1)):
+        q = torch.randn(T, H, 512, generator=g, device=cuda).to(torch.bfloat16)
+        idx = torch.randint(-40, n + 40, (T, 1, topk), generator=g, device=cuda, dtype=torch.int32)
+        idx[0, :, topk // 2:] = -1
+        log_case("mla pair kernel", T, H, topk, splits)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+        torch.cuda.synchronize()
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=1, block_n=32)
+        compare(out, want, ("pair kernel", T, H, topk, splits))
+        blank = triton_mla_sparse_attention(q, kv, torch.full_like(idx, -1), W.SM_SCALE, num_kv_splits=splits)
+        assert torch.equal(blank, torch.zeros_like(blank)), (T, H, topk, splits)
+    q = torch.randn(2, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+    idx = torch.randint(0, 100, (2, 1, 1024), generator=g, device=cuda, dtype=torch.int32)
+    empty = torch.zeros(0, 1, 528, dtype=torch.int8, device=cuda)
+    out = triton_mla_sparse_attention(q, empty, idx, W.SM_SCALE, num_kv_splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.zeros_like(out))
