@@ -544,17 +544,14 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   }
 }
 
-// ---------------------------------------------------------------- waves in pairs
-// A pair of waves runs one online-softmax stream over 32-key tiles -- the
-// loop structure of _sparse_mla_compute_tile with BLOCK_N = 32 -- and the two
-// waves split the latent: wave w of the pair gathers, converts and multiplies
-// latents [256 w, 256 w + 256) of every key.  A workgroup holds kPairs pairs
-// of one (split, token, 16-head group); the split's tiles are dealt to the
-// pairs in turn (tile n -> pair n % kPairs), and the pairs' streams meet in
-// LDS at the end (base-2 rescale to the largest max, summed in pair order).
-// kPairs = 1 is the reference's single stream per split (long splits: the
-// prefill-shaped call); more pairs put the tiles of a short decode split
-// into one round.
+// ---------------------------------------------------------------- long splits: waves in pairs
+// Splits of more than one chunk of flat-row indices (the prefill-shaped call:
+// one split of 2176 keys per token) take this kernel.  One workgroup of two
+// waves per (split, token, 16-head group) runs a single online-softmax stream
+// over the split's 32-key tiles in order -- the loop structure of
+// _sparse_mla_compute_tile with BLOCK_N = 32 -- and the two waves split the
+// latent: wave w gathers, converts and multiplies latents [256 w, 256 w + 256)
+// of every key.
 //   * S^T = K Q^T per 16-key half on v_mfma_f32_16x16x32_bf16 over the wave's
 //     256 latents (8 K-steps); the two waves' partial S^T meet in LDS (one
 //     barrier per tile) and both add them in the same order, so both run the
@@ -569,27 +566,21 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 //     registers).
 //   * The partial S^T buffer is single: a second barrier before a wave
 //     overwrites its half keeps it from racing the other wave's read.
-//   * Gathers run kRing tiles ahead and index loads 2 kRing; no barrier waits
+//   * Gathers run two tiles ahead and index loads four; no barrier waits
 //     for them (a workgroup barrier here waits only for LDS traffic).  Every
 //     load is unconditional: a masked key reads row 0 (its score becomes
 //     -1e30, its weight and scale 0, and int8 codes are finite); a branch
 //     around the loads would make the compiler's wait before the next use
 //     count no load as outstanding, draining the prefetch every tile.
-//   * 38 KB of LDS per pair.
+//   * 38 KB of LDS per workgroup and up to 512 registers per wave (280
+//     used; at two waves per SIMD the kernel spills).
 constexpr int kHalfLat = kLatent / 2;
 constexpr int kPairVStride = kHalfLat + 16;   // bf16 per LDS V row: 544 bytes
 constexpr int kPairRowBytes = kPairVStride * 2;
 
-template <int kPairs>
 struct __attribute__((aligned(16))) PairShared {
-  union {
-    uint16_t vbuf[2 * kPairs][kTile][kPairVStride];   // per wave: bf16 V half-rows of the tile
-    struct {
-      float rows[kPairs][kHeads][kRowStride];         // each pair's acc, row-major
-      float ml[kPairs][kHeads][2];                    // each pair's (m, l) per head
-    } fin;
-  };
-  float4 red[kPairs][2][2][64];                       // [pair][wave][key half][lane]: partial S^T
+  uint16_t vbuf[2][kTile][kPairVStride];      // per wave: bf16 V half-rows of the tile
+  float4 red[2][2][64];                       // [wave][key half][lane]: partial S^T
 };
 
 // Byte offset of bf16 element (row, col) of a wave's V buffer: 16-byte chunk
@@ -598,36 +589,23 @@ __device__ __forceinline__ int pair_vofs(int row, int col) {
   return row * kPairRowBytes + 16 * ((col >> 3) ^ ((row >> 3) & 1)) + 2 * (col & 7);
 }
 
-template <int kMode, int kPairs, int kRing>
-__global__ __launch_bounds__(128 * kPairs) __attribute__((amdgpu_waves_per_eu(kPairs == 1 ? 1 : 2, kPairs == 1 ? 1 : 2)))
+template <int kMode>
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void sparse_mla_pair_kernel(const MlaArgs a) {
   static_assert(kMode == kFlatRows, "the pair kernel reads flat cache rows");
-  static_assert(kRing == 1 || kRing == 2, "one or two tiles of gathers ahead");
-  __shared__ PairShared<kPairs> sh;
-  int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
-  if (kPairs > 1 && (gridDim.y * gridDim.z) % 8 == 0) {
-    // all splits of a (token, head group) unit on one XCD, where the merge
-    // kernel reads them back (see sparse_mla_kernel)
-    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int units = gridDim.y * gridDim.z;
-    split = lin / units;
-    t = (lin % units) % gridDim.y;
-    hg = (lin % units) / gridDim.y;
-  }
-  const int wv = uniform(threadIdx.x >> 6);
-  const int p = wv >> 1;          // pair
-  const int w = wv & 1;           // latent half of this wave
+  __shared__ PairShared sh;
+  const int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
+  const int w = uniform(threadIdx.x >> 6);   // latent half of this wave
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   const int c = lane & 15;
   const int start = split * a.split_len;
   const int end = min(start + a.split_len, a.topk);
   const int ntiles = end > start ? (end - start + kTile - 1) / kTile : 0;
-  const int niter = (ntiles + kPairs - 1) / kPairs;   // tiles per pair, the same for every pair
   const int head = hg * kHeads + c;
   const bool head_ok = head < a.num_heads;
   const int32_t* idx_t = a.idx + t * a.si_t;
-  uint8_t* vb = reinterpret_cast<uint8_t*>(&sh.vbuf[wv][0][0]);
+  uint8_t* vb = reinterpret_cast<uint8_t*>(&sh.vbuf[w][0][0]);
   // per-lane LDS bases (pair_vofs of the lane's first element)
   const int wr_lo = pair_vofs(c, 16 * g);        // row c, columns 16 g + [0, 8)
   const int wr_hi = pair_vofs(c, 16 * g + 8);    //        columns 16 g + 8 + [0, 8)
@@ -652,19 +630,19 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
   float m_run = kNegLarge, l_run = 0.f;
   bool acc_zero = true;
 
-  // The pair's j-th tile is tile p + kPairs j of the split.  Lane l < 32
-  // loads the index of key l of it, from a clamped address (no branch);
-  // issue_rows masks positions past the split.  (Masking here would make the
-  // wave wait for the load, and with it for every gather issued before it.)
-  auto tile_pos = [&](int j) { return start + (p + kPairs * j) * kTile + (lane & 31); };
-  auto load_idx = [&](int j) { return idx_t[min(tile_pos(j), end - 1)]; };
+  // Lane l < 32 loads the index of key l of tile n, from a clamped address
+  // (no branch); issue_rows masks positions past the split.  (Masking here
+  // would make the wave wait for the load, and with it for every gather
+  // issued before it.)
+  auto tile_pos = [&](int n) { return start + n * kTile + (lane & 31); };
+  auto load_idx = [&](int n) { return idx_t[min(tile_pos(n), end - 1)]; };
   struct Rows {
     uint4 d[2][4];      // [key half][chunk i]: latents 256 w + 64 i + 16 g + [0, 16) of key 16 u + c
     float sv;           // lane l < 32: scale of key l (garbage for a masked key)
     uint32_t vmask;     // bit l: key l valid
   };
-  auto issue_rows = [&](Rows& r, int raw, int j) {
-    const int pos = tile_pos(j);
+  auto issue_rows = [&](Rows& r, int raw, int n) {
+    const int pos = tile_pos(n);
     const int v = pos < end && raw >= 0 && static_cast<int64_t>(raw) < a.seq_kv ? raw : -1;
     // the scale first: older than the rows, its wait comes free with theirs
     r.sv = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(max(v, 0)) * a.skv + kLatent);
@@ -678,9 +656,9 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
     r.vmask = static_cast<uint32_t>(__ballot(lane < kTile && v >= 0));
   };
 
-  // One tile: convert + S^T + V to LDS, then the gathers kRing tiles on,
-  // then the exchange, softmax and PV.
-  auto tile = [&](int j, Rows& cur, int& idx_ahead) {
+  // One tile: convert + S^T + V to LDS, then the gathers two tiles on, then
+  // the exchange, softmax and PV.
+  auto tile = [&](int n, Rows& cur, int& idx_ahead) {
     f32x4 s_part[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -699,8 +677,8 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
       s_part[u] = sacc;
     }
     __syncthreads();   // the other wave has read this wave's previous partial
-    sh.red[p][w][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
-    sh.red[p][w][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
+    sh.red[w][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
+    sh.red[w][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
     // scales of the lane's keys 16 u + 4 g + r (0 for a masked key), and the validity bits
     float sc[8];
     const uint32_t kv_ok = ((cur.vmask >> (4 * g)) & 0xfu) | (((cur.vmask >> (16 + 4 * g)) & 0xfu) << 4);
@@ -711,19 +689,19 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
         const float v = __shfl(cur.sv, 16 * u + 4 * g + r, 64);
         sc[4 * u + r] = (kv_ok >> (4 * u + r)) & 1 ? v : 0.f;
       }
-    // the registers of this tile are free: gathers kRing tiles on, index 2 kRing on
+    // the registers of this tile are free: gathers of tile n + 2, index of tile n + 4
     // (kept below the conversions: hoisted above them the loads would hold a
     // second tile's registers while the converted operands are still live)
     __builtin_amdgcn_sched_barrier(0);
-    issue_rows(cur, idx_ahead, j + kRing);
-    idx_ahead = load_idx(j + 2 * kRing);
+    issue_rows(cur, idx_ahead, n + 2);
+    idx_ahead = load_idx(n + 4);
     __syncthreads();
 
     // Full scores: wave 0's partial + wave 1's, the same order in both waves.
     float s[8];
     {
-      const float4 p00 = sh.red[p][0][0][lane], p01 = sh.red[p][0][1][lane];
-      const float4 p10 = sh.red[p][1][0][lane], p11 = sh.red[p][1][1][lane];
+      const float4 p00 = sh.red[0][0][lane], p01 = sh.red[0][1][lane];
+      const float4 p10 = sh.red[1][0][lane], p11 = sh.red[1][1][lane];
       const float4 h0[2] = {p00, p01}, h1[2] = {p10, p11};
 #pragma unroll
       for (int jj = 0; jj < 8; jj++) {
@@ -773,119 +751,39 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
     acc_zero = false;
   };
 
-  // Every pair runs niter tiles (a tile past the split is fully masked and
-  // changes nothing): the barriers of all waves match.  With two tiles of
-  // gathers ahead the tiles go in pairs -- no branch in the loop body.
-  if (kRing == 2) {
-    Rows ra, rb;
-    int ia = -1, ib = -1;   // index of tile j + 2 (j even: ia, odd: ib), then j + 4 after use
-    if (niter > 0) {
-      const int i0 = load_idx(0), i1 = load_idx(1);
-      ia = load_idx(2);
-      ib = load_idx(3);
-      issue_rows(ra, i0, 0);
-      issue_rows(rb, i1, 1);
-    }
-    for (int j = 0; j < niter; j += 2) {
-      tile(j, ra, ia);
-      tile(j + 1, rb, ib);
-    }
-  } else {
-    Rows ra;
-    int ia = -1;            // index of tile j + 1, then j + 2 after use
-    if (niter > 0) {
-      const int i0 = load_idx(0);
-      ia = load_idx(1);
-      issue_rows(ra, i0, 0);
-    }
-    for (int j = 0; j < niter; j++) tile(j, ra, ia);
+  // Tiles go in pairs (an odd count ends with a fully masked tile, which
+  // changes nothing): no branch in the loop body.
+  Rows ra, rb;
+  int ia = -1, ib = -1;   // index of tile n + 2 (n even: ia, odd: ib), then n + 4 after use
+  if (ntiles > 0) {
+    const int i0 = load_idx(0), i1 = load_idx(1);
+    ia = load_idx(2);
+    ib = load_idx(3);
+    issue_rows(ra, i0, 0);
+    issue_rows(rb, i1, 1);
+  }
+  for (int n = 0; n < ntiles; n += 2) {
+    tile(n, ra, ia);
+    tile(n + 1, rb, ib);
   }
 
-  if (kPairs == 1) {
-    // Both waves hold the same m and l; each writes its latent half.
-    const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
-    if (!head_ok) return;
-    if (a.num_splits == 1 && !a.partials_only) {
-      uint16_t* op = a.out + t * a.so_t + head * a.so_h + kHalfLat * w + 4 * g;
-#pragma unroll
-      for (int dt = 0; dt < 16; dt++)
-        *reinterpret_cast<uint2*>(op + 16 * dt) = make_uint2(pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l),
-                                                             pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l));
-    } else {
-      const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
-      float* pp = a.part + row * kLatent + kHalfLat * w + 4 * g;
-#pragma unroll
-      for (int dt = 0; dt < 16; dt++)
-        *reinterpret_cast<float4*>(pp + 16 * dt) = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l,
-                                                               acc[dt][2] * inv_l, acc[dt][3] * inv_l);
-      if (w == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
-    }
-    return;
-  }
-
-  // kPairs > 1: the pairs park their accumulators row-major in LDS, then every
-  // wave finishes whole result rows (m = max over pairs, base-2 rescale,
-  // summed in pair order, 1 / l) with contiguous stores.
-  __syncthreads();   // V buffers are free
-  {
-    float* rp = &sh.fin.rows[p][c][kHalfLat * w + 4 * g];
+  // Both waves hold the same m and l; each writes its latent half.
+  const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
+  if (!head_ok) return;
+  if (a.num_splits == 1 && !a.partials_only) {
+    uint16_t* op = a.out + t * a.so_t + head * a.so_h + kHalfLat * w + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 16; dt++)
-      *reinterpret_cast<float4*>(rp + 16 * dt) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
-    if (w == 0 && g == 0) {
-      sh.fin.ml[p][c][0] = m_run;
-      sh.fin.ml[p][c][1] = l_run;
-    }
-  }
-  __syncthreads();
-  constexpr int kRowsPerWave = kHeads / (2 * kPairs);
+      *reinterpret_cast<uint2*>(op + 16 * dt) = make_uint2(pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l),
+                                                           pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l));
+  } else {
+    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
+    float* pp = a.part + row * kLatent + kHalfLat * w + 4 * g;
 #pragma unroll
-  for (int k = 0; k < kRowsPerWave; k++) {
-    const int r = kRowsPerWave * wv + k;    // result row (head in the group), uniform per wave
-    const int hd = hg * kHeads + r;
-    if (hd >= a.num_heads) break;
-    float mm = kNegLarge;
-#pragma unroll
-    for (int q = 0; q < kPairs; q++) mm = fmaxf(mm, sh.fin.ml[q][r][0]);
-    float fs[kPairs];
-    float l = 0.f;
-#pragma unroll
-    for (int q = 0; q < kPairs; q++) {
-      fs[q] = fast_exp2(sh.fin.ml[q][r][0] - mm);
-      l += sh.fin.ml[q][r][1] * fs[q];
-    }
-    const float inv_l = 1.f / (l > 0.f ? l : 1.f);
-    auto fin4 = [&](int col) {
-      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-      for (int q = 0; q < kPairs; q++) {
-        const float4 x = *reinterpret_cast<const float4*>(&sh.fin.rows[q][r][col]);
-        o.x += x.x * fs[q]; o.y += x.y * fs[q]; o.z += x.z * fs[q]; o.w += x.w * fs[q];
-      }
-      return make_float4(o.x * inv_l, o.y * inv_l, o.z * inv_l, o.w * inv_l);
-    };
-    if (a.num_splits == 1 && !a.partials_only) {
-      const float4 u = fin4(8 * lane);
-      const float4 v = fin4(8 * lane + 4);
-      uint4 o;
-      o.x = pack_bf16x2(u.x, u.y);
-      o.y = pack_bf16x2(u.z, u.w);
-      o.z = pack_bf16x2(v.x, v.y);
-      o.w = pack_bf16x2(v.z, v.w);
-      uint16_t* op = a.out + t * a.so_t + hd * a.so_h + 8 * lane;
-      if (a.out_align16) {
-        *reinterpret_cast<uint4*>(op) = o;
-      } else {
-        reinterpret_cast<uint2*>(op)[0] = make_uint2(o.x, o.y);
-        reinterpret_cast<uint2*>(op)[1] = make_uint2(o.z, o.w);
-      }
-    } else {
-      const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + hd;
-      float* pp = a.part + row * kLatent;
-      *reinterpret_cast<float4*>(pp + 4 * lane) = fin4(4 * lane);
-      *reinterpret_cast<float4*>(pp + 256 + 4 * lane) = fin4(256 + 4 * lane);
-      if (lane == 0) a.lse[row] = (mm + log2f(l)) * kLn2;
-    }
+    for (int dt = 0; dt < 16; dt++)
+      *reinterpret_cast<float4*>(pp + 16 * dt) = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l,
+                                                             acc[dt][2] * inv_l, acc[dt][3] * inv_l);
+    if (w == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
   }
 }
 
@@ -1178,7 +1076,7 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   } else if (mode == kPagedPos) {
     if (pipe) GLM53_LAUNCH(kPagedPos, true); else GLM53_LAUNCH(kPagedPos, false);
   } else if (pipe && a.seq_kv > 0) {   // (its masked keys read row 0)
-    hipLaunchKernelGGL((sparse_mla_pair_kernel<kFlatRows, 1, 2>), grid, dim3(128), 0, st, a);
+    hipLaunchKernelGGL((sparse_mla_pair_kernel<kFlatRows>), grid, dim3(128), 0, st, a);
   } else {
     if (pipe) GLM53_LAUNCH(kFlatRows, true); else GLM53_LAUNCH(kFlatRows, false);
   }
