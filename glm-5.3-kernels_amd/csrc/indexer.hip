@@ -219,6 +219,128 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
   }
 }
 
+// Rows that share one block table (the query rows of one request's prefill
+// chunk, each with its own causal length): workgroup = (run of kN 16-key
+// groups, 16 rows); wave w scores rows 4w .. 4w + 3 of the block over the
+// run, so each key group is loaded once per wave and used for 4 rows x
+// kTiles head tiles, and the four waves load the same groups (the later
+// waves' loads hit the CU's L1) -- the keys are read from L2 once per 16 rows
+// instead of once per row.  Same arithmetic per (row, key) as the per-token
+// kernel above; block sizes that are a multiple of 16 only.
+template <int kTiles, int kN>
+__global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(const LogitsArgs a, int num_tokens) {
+  constexpr int kR = 4;        // rows per wave
+  constexpr int kDepth = 4;
+  const int lane = threadIdx.x & 63;
+  const int w = uniform(threadIdx.x >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int t0 = blockIdx.y * (kR * kLogitWaves) + kR * w;   // first row of this wave
+  const int j_run = blockIdx.x * a.keys_per_wg;
+  const int j_end = j_run + 16 * kN < a.max_len ? j_run + 16 * kN : a.max_len;
+  const int n = (j_end - j_run + 15) / 16;
+  const int cap = a.max_blocks * a.block_size;
+  int len[kR];
+  int len_max = 0;
+#pragma unroll
+  for (int r = 0; r < kR; r++) {
+    int l = t0 + r < num_tokens ? a.ctx[t0 + r] : 0;
+    l = l < 0 ? 0 : l > cap ? cap : l;
+    len[r] = l;
+    len_max = len_max > l ? len_max : l;
+  }
+
+  // page of each group's first key (lane i < n: group i; -1 past every row's context)
+  int blk_l = -1;
+  if (lane < n) {
+    const int j0 = j_run + 16 * lane;
+    if (j0 < len_max) blk_l = a.bt[j0 / a.block_size];
+  }
+
+  // q fragments (A operand) and weights of this lane's heads, per row
+  uint64_t qf[kR][kTiles][4];
+  float wv[kR][kTiles][4];
+#pragma unroll
+  for (int r = 0; r < kR; r++) {
+    const int t = t0 + r < num_tokens ? t0 + r : num_tokens - 1;   // rows past the end: loaded, never stored
+#pragma unroll
+    for (int ht = 0; ht < kTiles; ht++) {
+      const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (16 * ht + c) * a.sq_h + 16 * g);
+      const uint4 lo = qp[0], hi = qp[4];
+      qf[r][ht][0] = (static_cast<uint64_t>(lo.y) << 32) | lo.x;
+      qf[r][ht][1] = (static_cast<uint64_t>(lo.w) << 32) | lo.z;
+      qf[r][ht][2] = (static_cast<uint64_t>(hi.y) << 32) | hi.x;
+      qf[r][ht][3] = (static_cast<uint64_t>(hi.w) << 32) | hi.z;
+#pragma unroll
+      for (int i = 0; i < 4; i++) wv[r][ht][i] = a.w[t * a.sw_t + 16 * ht + 4 * g + i];
+    }
+  }
+
+  __shared__ float res[kLogitWaves][kR][16 * kN];
+  __shared__ uint8_t put[kLogitWaves][kR][16 * kN];   // 1: write res, 0: leave the position untouched
+  Group ring[kDepth];
+  // group i of the run, or past the run's end its last group again (loaded, not used)
+  auto load = [&](int i, Group& gr) {
+    const int ic = i < n ? i : n - 1;
+    load_group<true>(a, 0, j_run + 16 * ic, __builtin_amdgcn_readlane(blk_l, ic), len_max, g, c, gr);
+  };
+  if (n > 0) {
+#pragma unroll
+    for (int s = 0; s < kDepth - 1; s++)
+      if (s < kN) load(s, ring[s]);
+#pragma unroll
+    for (int i = 0; i < kN; i++) {
+      if (i + kDepth - 1 < kN) load(i + kDepth - 1, ring[(i + kDepth - 1) % kDepth]);
+      if (i >= n) continue;   // uniform (the tail of the rows)
+      const Group& gr = ring[i % kDepth];
+      const int j = j_run + 16 * i + c;
+      float v[kR] = {};
+      if (gr.live) {
+        const uint64_t k0 = (static_cast<uint64_t>(gr.kd[0].y) << 32) | gr.kd[0].x;
+        const uint64_t k1 = (static_cast<uint64_t>(gr.kd[0].w) << 32) | gr.kd[0].z;
+        const uint64_t k2 = (static_cast<uint64_t>(gr.kd[1].y) << 32) | gr.kd[1].x;
+        const uint64_t k3 = (static_cast<uint64_t>(gr.kd[1].w) << 32) | gr.kd[1].z;
+#pragma unroll
+        for (int r = 0; r < kR; r++) {
+          const float sc = gr.kok && j < len[r] ? gr.sc : 0.f;
+#pragma unroll
+          for (int ht = 0; ht < kTiles; ht++) {
+            f32x4v d = {0.f, 0.f, 0.f, 0.f};
+            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][0]), static_cast<long>(k0), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][1]), static_cast<long>(k1), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][2]), static_cast<long>(k2), d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][3]), static_cast<long>(k3), d, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[r] = __builtin_fmaf(wv[r][ht][e], fmaxf(sc * d[e], 0.f), v[r]);
+          }
+          v[r] = row_sum4(v[r]);
+        }
+      }
+      if (g == 0) {
+#pragma unroll
+        for (int r = 0; r < kR; r++) {
+          const bool ok = gr.kok && j < len[r];
+          // page outside the cache, or past the row's context: -inf (past the context only when cleaning)
+          res[w][r][16 * i + c] = ok ? v[r] : -__builtin_inff();
+          put[w][r][16 * i + c] = j < j_end && (j < len[r] || a.clean);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int r = 0; r < kR; r++) {
+    if (t0 + r >= num_tokens) break;   // uniform
+    float* out = a.logits + (t0 + r) * a.sl_t;
+#pragma unroll
+    for (int q = 0; q < (16 * kN + 63) / 64; q++) {
+      const int idx = 64 * q + lane;
+      if (idx < 16 * n && put[w][r][idx]) out[j_run + idx] = res[w][r][idx];
+    }
+  }
+}
+
 // ------------------------------------------------------------------ top-k
 constexpr int kHistBins = 4096;
 constexpr int kChunkThreads = 512;
@@ -673,7 +795,8 @@ extern "C" int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t s
       num_tokens > 65535 || block_size < 1 || num_blocks < 1 || num_blocks > (int64_t(1) << 31) - 1 ||
       max_blocks < 1 || max_len < 0 || max_len > (int64_t(1) << 30) ||
       max_blocks * block_size > (int64_t(1) << 31) - 1 || page_bytes < block_size * (kHeadDim + 4) ||
-      sq_h < kHeadDim || sq_t < num_heads * sq_h || sw_t < num_heads || sl_t < max_len || bt_stride < max_blocks)
+      sq_h < kHeadDim || sq_t < num_heads * sq_h || sw_t < num_heads || sl_t < max_len ||
+      (bt_stride != 0 && bt_stride < max_blocks))
     return GLM53_ERR_BAD_SHAPE;
   if (!aligned(q, 16) || sq_t % 16 || sq_h % 16 || !aligned(kv_cache, 16) || page_bytes % 16 ||
       (block_size * kHeadDim) % 4 || !aligned(weights, 4) || !aligned(logits, 4))
@@ -683,6 +806,27 @@ extern "C" int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t s
   // rows (one resident round at 2 workgroups per CU), 1 to 16 groups; one
   // group when groups straddle pages (block_size % 16 != 0).
   const bool al = block_size % 16 == 0;
+  if (bt_stride == 0 && al && num_tokens >= 16) {
+    // one table shared by every row (a request's prefill chunk): 16 rows per workgroup
+    constexpr int kRowsN = 16;
+    LogitsArgs a{static_cast<const uint8_t*>(q), sq_t, sq_h, static_cast<const uint8_t*>(kv_cache), page_bytes,
+                 static_cast<int>(block_size), static_cast<int>(num_blocks), weights, sw_t, context_lens,
+                 block_table, 0, static_cast<int>(max_blocks), static_cast<int>(num_heads),
+                 static_cast<int>(max_len), 16 * kRowsN, logits, sl_t, clean_logits ? 1 : 0};
+    const dim3 grid(static_cast<unsigned>((max_len + 16 * kRowsN - 1) / (16 * kRowsN)),
+                    static_cast<unsigned>((num_tokens + 4 * kLogitWaves - 1) / (4 * kLogitWaves)));
+    void (*kernel)(LogitsArgs, int);
+    switch (num_heads / 16) {
+      case 1: kernel = fp8_mqa_logits_rows_kernel<1, kRowsN>; break;
+      case 2: kernel = fp8_mqa_logits_rows_kernel<2, kRowsN>; break;
+      case 3: kernel = fp8_mqa_logits_rows_kernel<3, kRowsN>; break;
+      default: kernel = fp8_mqa_logits_rows_kernel<4, kRowsN>; break;
+    }
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(kernel, grid, dim3(kLogitThreads), 0, static_cast<hipStream_t>(stream), a,
+                       static_cast<int>(num_tokens));
+    return static_cast<int>(hipGetLastError());
+  }
   const int64_t groups = num_tokens * ((max_len + 15) / 16);
   int gpw = 1;
   while (al && gpw < 16 && groups >= int64_t(kLogitWaves) * 512 * gpw * 2) gpw *= 2;

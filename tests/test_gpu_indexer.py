@@ -351,3 +351,39 @@ def test_prefill_shape_sampled_rows(cuda, oracle):
                  lens.index_select(0, sel), bt.index_select(0, sel), pools, clean=False)
     want = oracle.indexer_topk(logits.cpu().numpy(), lens.cpu().numpy(), 512)
     assert np.array_equal(top.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("heads", [16, 32, 64])
+def test_shared_table_rows_kernel(cuda, oracle, heads):
+    """Rows sharing one block table (row stride 0: a request's prefill
+    chunk) take the row-tiled logits kernel: bit-identical to the per-token
+    kernel on the same table materialised per row, and against the oracle;
+    37 rows (not a multiple of the 16-row block) with lengths 0, short, odd,
+    past the table, and the full context, a padded page stride and one table
+    entry outside the cache, clean and not."""
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits
+    g = torch.Generator(device=cuda).manual_seed(300 + heads)
+    bs, pools = 64, 2500
+    cache, nb = W.indexer_cache(cuda, g, pools + 200, bs, page_pad=32)
+    per_req = (pools + bs - 1) // bs
+    table = torch.randperm(nb, generator=g, device=cuda).to(torch.int32)[:per_req]
+    table[5] = nb + 3                                   # outside the cache: its keys are -inf
+    T = 37
+    lens = torch.randint(0, pools + 1, (T,), generator=g, device=cuda, dtype=torch.int32)
+    lens[:6] = torch.tensor([0, 1, 17, pools, pools + 500, 1000], dtype=torch.int32, device=cuda)
+    qf = torch.randn(T, 1, heads, 128, generator=g, device=cuda)
+    q = (qf * (448.0 / qf.abs().amax(dim=-1, keepdim=True))).to(torch.float8_e4m3fn)
+    w = (torch.randn(T, heads, generator=g, device=cuda) * heads ** -0.5).contiguous()
+    shared = table[None, :].expand(T, per_req)
+    for clean in (True, False):
+        log_case("indexer shared-table rows", heads, clean)
+        got = fp8_paged_mqa_logits(q, cache, w, lens, shared, pools, clean_logits=clean)
+        ref = fp8_paged_mqa_logits(q, cache, w, lens, shared.contiguous(), pools, clean_logits=clean)
+        torch.cuda.synchronize()
+        if clean:
+            assert torch.equal(got, ref)
+        else:   # unwritten positions hold whatever torch.empty gave: compare the written ones
+            n = torch.arange(pools, device=cuda)[None, :] < lens.clamp(max=pools)[:, None].long()
+            assert torch.equal(got[n], ref[n])
+        check_logits(oracle, got, q, cache, w, lens, shared.contiguous(), pools, clean, rows=range(0, T, 6))

@@ -267,13 +267,13 @@ def indexer_prefill_inputs(device, g, rows=2048, context=262144, block_size=64, 
     the complete pools before them, 65536 pools of 4 tokens in 1024 pages of
     64 placed at random.  Returns (q fp8 [rows, 1, H, 128], cache, weights
     fp32 [rows, H], context_lens int32 [rows] = (position + 1) // 4,
-    block_table int32 [rows, 1024] (the request's table on every row),
-    max_model_len (pools))."""
+    block_table int32 [rows, 1024] (the request's table as a stride-0 view:
+    every row reads the same table), max_model_len (pools))."""
     pools = context // INDEX_KPOOL
     per_req = (pools + block_size - 1) // block_size
     cache, nb = indexer_cache(device, g, pools, block_size)
     table = torch.randperm(nb, generator=g, device=device).to(torch.int32)[:per_req]
-    bt = table[None, :].expand(rows, per_req).contiguous()
+    bt = table[None, :].expand(rows, per_req)   # one table, shared by every row (row stride 0)
     qf = torch.randn(rows, 1, heads, INDEX_DIM, generator=g, device=device)
     q = (qf * (448.0 / qf.abs().amax(dim=-1, keepdim=True))).to(torch.float8_e4m3fn)
     w = torch.randn(rows, heads, generator=g, device=device) * heads ** -0.5
