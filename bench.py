@@ -141,6 +141,15 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
         kv1 = cache1.view(n_rows, 1, W.ROW_BYTES)
         fn = lambda: triton_mla_sparse_attention(q1, kv1, idx1, W.SM_SCALE, num_kv_splits=args.splits)
         nbytes = W.mla_bytes(idx1, n_rows)
+    elif args.case == "indexer_prefill":
+        # 2048 query rows at the end of a 262144-token context: logits over
+        # 65536 pools, then the top 512 per row
+        from sparse_indexer import fp8_paged_mqa_logits, indexer_topk
+        gi = W.gen(dev, W.SEED_BENCH + 2048)
+        qpi, cpi, wpi, lpi, bpi, npi = W.indexer_prefill_inputs(dev, gi)
+        fn = lambda: indexer_topk(fp8_paged_mqa_logits(qpi, cpi, wpi, lpi, bpi, npi, clean_logits=False), lpi,
+                                  W.INDEX_TOPK_POOLS)
+        nbytes = W.indexer_bytes(lpi)
     else:   # decode_b8_split: the split kernel alone at the auto split count
         s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
         fn = lambda: sparse_mla_partials(q8, next_cache(), idx8, W.SM_SCALE, s8)
@@ -164,7 +173,8 @@ def main():
     ap.add_argument("--rotate", type=int, default=1,
                     help="with --case prefill / decode_b8_split: cycle the calls over this many 262144-row "
                          "caches (HBM-resident when their total exceeds the 256 MB MALL)")
-    ap.add_argument("--case", choices=("writer_scattered", "prefill", "decode_b1", "decode_b8_split"),
+    ap.add_argument("--case", choices=("writer_scattered", "prefill", "decode_b1", "decode_b8_split",
+                                       "indexer_prefill"),
                     default=None,
                     help="time one workload alone (K calls, one per graph replay unless --unroll), print "
                          "its figure to stderr and exit: the command behind a kernel profile")

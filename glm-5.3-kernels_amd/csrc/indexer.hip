@@ -18,16 +18,16 @@
 //
 // Logits kernel: workgroup = (token, run of keys); 4 wavefronts, each takes
 // a run of 16-key groups.  Per group: the 16 keys' 128 bytes (one contiguous
-// 2 KB block when the keys share a page) and scales, then 4 x (H/16)
-// v_mfma_f32_16x16x32_fp8_fp8 with A = q (16 heads x 32 dims), B = k^T
-// (32 dims x 16 keys).  Lane (g, c) of D holds key c for heads 4g + [0, 4)
-// of each head tile, so the relu-weighted head sum is 4 FMAs per tile and
-// two cross-row swaps.  Each lane's B operand is dims [16g, 16g + 16) and
-// [64 + 16g, 64 + 16g + 16) of key c and the A operand the same dims of its
-// head: k-slot 8g + e of MFMA m is dim 16g + 8m + e (m < 2), 64 + 16g +
-// 8(m - 2) + e (m >= 2) on both sides, so each of the two 16-byte load
-// instructions covers whole 64-byte halves of its 16 keys' lines (each half
-// requested once, however soon the L1 evicts it).  A wave reads
+// 2 KB block when the keys share a page) and scales, then per head tile one
+// v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales) with A = q (16 heads x
+// 128 dims), B = k^T (128 dims x 16 keys).  Lane (g, c) of D holds key c for
+// heads 4g + [0, 4) of each head tile, so the relu-weighted head sum is 4
+// FMAs per tile and two cross-row swaps.  Each lane's B operand is dims
+// [16g, 16g + 16) and [64 + 16g, 64 + 16g + 16) of key c and the A operand
+// the same dims of its head: k-slot 32g + 8m + e is dim 16g + 8m + e
+// (m < 2), 64 + 16g + 8(m - 2) + e (m >= 2) on both sides, so each of the
+// two 16-byte load instructions covers whole 64-byte halves of its 16 keys'
+// lines (each half requested once, however soon the L1 evicts it).  A wave reads
 // its groups' block-table entries at once and streams the groups through a
 // register ring with three groups' loads in flight.
 //
@@ -80,6 +80,25 @@ __device__ __forceinline__ float row_sum4(float v) {
   v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// A lane's 32 bytes of a key (dims 16g + [0, 16) and 64 + 16g + [0, 16)) as
+// the B operand of the K = 128 FP8 product.
+__device__ __forceinline__ i32x8 key_operand(uint64_t k0, uint64_t k1, uint64_t k2, uint64_t k3) {
+  return i32x8{static_cast<int>(k0), static_cast<int>(k0 >> 32), static_cast<int>(k1), static_cast<int>(k1 >> 32),
+               static_cast<int>(k2), static_cast<int>(k2 >> 32), static_cast<int>(k3), static_cast<int>(k3 >> 32)};
+}
+
+// q . k for 16 heads x 16 keys over all 128 dims in one
+// v_mfma_scale_f32_16x16x128_f8f6f4 (both operands FP8 E4M3, unit E8M0
+// scales): lane (g, c) gives the same 32 dims of its head (A) and of its key
+// (B), so every q byte meets the k byte of the same dim.
+__device__ __forceinline__ f32x4v dot128_fp8(const uint64_t (&q)[4], const i32x8& kb) {
+  const i32x8 qa = key_operand(q[0], q[1], q[2], q[3]);
+  const f32x4v zero = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa, kb, zero, 0, 0, 0, 127, 0, 127);
 }
 
 // Loads of one 16-key group (keys j0 + c) into registers: the 32 key bytes
@@ -190,13 +209,10 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
         const uint64_t k1 = (static_cast<uint64_t>(gr.kd[0].w) << 32) | gr.kd[0].z;
         const uint64_t k2 = (static_cast<uint64_t>(gr.kd[1].y) << 32) | gr.kd[1].x;
         const uint64_t k3 = (static_cast<uint64_t>(gr.kd[1].w) << 32) | gr.kd[1].z;
+        const i32x8 kb = key_operand(k0, k1, k2, k3);
 #pragma unroll
         for (int ht = 0; ht < kTiles; ht++) {
-          f32x4v d = {0.f, 0.f, 0.f, 0.f};
-          d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][0]), static_cast<long>(k0), d, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][1]), static_cast<long>(k1), d, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][2]), static_cast<long>(k2), d, 0, 0, 0);
-          d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[ht][3]), static_cast<long>(k3), d, 0, 0, 0);
+          const f32x4v d = dot128_fp8(qf[ht], kb);
 #pragma unroll
           for (int e = 0; e < 4; e++) v = __builtin_fmaf(wv[ht][e], fmaxf(sc * d[e], 0.f), v);
         }
@@ -299,16 +315,13 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(cons
         const uint64_t k1 = (static_cast<uint64_t>(gr.kd[0].w) << 32) | gr.kd[0].z;
         const uint64_t k2 = (static_cast<uint64_t>(gr.kd[1].y) << 32) | gr.kd[1].x;
         const uint64_t k3 = (static_cast<uint64_t>(gr.kd[1].w) << 32) | gr.kd[1].z;
+        const i32x8 kb = key_operand(k0, k1, k2, k3);
 #pragma unroll
         for (int r = 0; r < kR; r++) {
           const float sc = gr.kok && j < len[r] ? gr.sc : 0.f;
 #pragma unroll
           for (int ht = 0; ht < kTiles; ht++) {
-            f32x4v d = {0.f, 0.f, 0.f, 0.f};
-            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][0]), static_cast<long>(k0), d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][1]), static_cast<long>(k1), d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][2]), static_cast<long>(k2), d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(static_cast<long>(qf[r][ht][3]), static_cast<long>(k3), d, 0, 0, 0);
+            const f32x4v d = dot128_fp8(qf[r][ht], kb);
 #pragma unroll
             for (int e = 0; e < 4; e++) v[r] = __builtin_fmaf(wv[r][ht][e], fmaxf(sc * d[e], 0.f), v[r]);
           }

@@ -592,7 +592,7 @@ __device__ __forceinline__ int pair_vofs(int row, int col) {
 template <int kMode>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void sparse_mla_pair_kernel(const MlaArgs a) {
-  static_assert(kMode == kFlatRows, "the pair kernel reads flat cache rows");
+  constexpr bool kPaged = kMode != kFlatRows;
   __shared__ PairShared sh;
   const int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
   const int w = uniform(threadIdx.x >> 6);   // latent half of this wave
@@ -605,6 +605,19 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
   const int head = hg * kHeads + c;
   const bool head_ok = head < a.num_heads;
   const int32_t* idx_t = a.idx + t * a.si_t;
+  // Paged modes: the request's block-table row.  Every table read below is
+  // unconditional, from an address clamped into that row; a request id
+  // outside the table (or a zero-width table) reads req_id[t] instead and
+  // maps every key to -1.
+  const int req = kPaged ? a.req_id[t] : 0;
+  const bool req_ok = kPaged && req >= 0 && req < a.num_reqs && a.max_blocks > 0;
+  const int32_t* bt_req = req_ok ? a.bt + static_cast<int64_t>(req) * a.bt_stride : a.req_id + t;
+  const int max_blocks = req_ok ? a.max_blocks : 0;
+  const int last_blk = max(max_blocks, 1) - 1;
+  // Pooled mode: the token's pool ids (with none, req_id[t] stands in and is never used)
+  const int32_t* pools_t = kMode == kPooledPos && a.num_pools > 0 ? a.pools + t * a.sp_t : a.req_id + t;
+  const int last_pool = max(a.num_pools, 1) - 1;
+  const int seq_len_t = kMode == kPooledPos && a.seq_lens ? a.seq_lens[t] : -1;
   uint8_t* vb = reinterpret_cast<uint8_t*>(&sh.vbuf[w][0][0]);
   // per-lane LDS bases (pair_vofs of the lane's first element)
   const int wr_lo = pair_vofs(c, 16 * g);        // row c, columns 16 g + [0, 8)
@@ -630,35 +643,80 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
   float m_run = kNegLarge, l_run = 0.f;
   bool acc_zero = true;
 
-  // Lane l < 32 loads the index of key l of tile n, from a clamped address
-  // (no branch); issue_rows masks positions past the split.  (Masking here
-  // would make the wave wait for the load, and with it for every gather
-  // issued before it.)
+  // Key l of tile n is handled by lane l < 32 in three steps, each one tile
+  // ahead of the next so that no step waits for a load younger than the
+  // gathers in flight (loads complete in order):
+  //   load_raw (tile n - 4): its index (pooled mode: its pool id), read
+  //     from an address clamped into the split, with no branch;
+  //   lookup   (tile n - 3): the position's block-table entry (paged modes;
+  //     flat rows need no load), again from a clamped address;
+  //   issue_rows (tile n - 2): the scale and the row gathers.
+  // Positions past the split and invalid keys are masked in lookup and
+  // issue_rows; masked keys read row 0 (unit 0 of the paged cache), which
+  // exists because the launch requires a non-empty cache.  (Masking right
+  // after a load would make the wave wait for it, and with it for every
+  // gather issued before it.)
   auto tile_pos = [&](int n) { return start + n * kTile + (lane & 31); };
-  auto load_idx = [&](int n) { return idx_t[min(tile_pos(n), end - 1)]; };
+  auto load_raw = [&](int n) {
+    const int k = min(tile_pos(n), end - 1);
+    if constexpr (kMode == kPooledPos) return pools_t[min(k / a.pool_size, last_pool)];
+    else return idx_t[k];
+  };
+  struct Look {
+    int e;     // flat: the row or -1; paged: the block-table entry (checked in issue_rows)
+    int rel;   // paged: the row within its page, or -1 for a masked key
+  };
+  auto lookup = [&](int raw, int n) {
+    const int pos = tile_pos(n);
+    Look l;
+    if constexpr (kMode == kFlatRows) {
+      l.e = pos < end && raw >= 0 && static_cast<int64_t>(raw) < a.seq_kv ? raw : -1;
+      l.rel = 0;
+    } else {
+      int p = raw;   // request-relative position (pooled_position for the pooled layout)
+      if constexpr (kMode == kPooledPos) {
+        const int expanded = a.num_pools * a.pool_size;
+        const int j = pos - expanded;
+        const int pq = pos / a.pool_size;
+        p = pos < expanded ? (raw >= 0 ? raw * a.pool_size + (pos - pq * a.pool_size) : -1)
+            : seq_len_t >= 0 && j < a.pool_size - 1 && j < seq_len_t % a.pool_size
+                ? seq_len_t / a.pool_size * a.pool_size + j
+                : -1;
+      }
+      const int blk = static_cast<int>(static_cast<uint32_t>(max(p, 0)) / static_cast<uint32_t>(a.block_size));
+      l.e = bt_req[min(blk, last_blk)];
+      l.rel = pos < end && p >= 0 && blk < max_blocks ? p - blk * a.block_size : -1;
+    }
+    return l;
+  };
   struct Rows {
     uint4 d[2][4];      // [key half][chunk i]: latents 256 w + 64 i + 16 g + [0, 16) of key 16 u + c
     float sv;           // lane l < 32: scale of key l (garbage for a masked key)
     uint32_t vmask;     // bit l: key l valid
   };
-  auto issue_rows = [&](Rows& r, int raw, int n) {
-    const int pos = tile_pos(n);
-    const int v = pos < end && raw >= 0 && static_cast<int64_t>(raw) < a.seq_kv ? raw : -1;
+  // flat: row index, rows skv bytes apart; paged: 16-byte unit of the row
+  const int64_t unit_bytes = kPaged ? 16 : a.skv;
+  auto issue_rows = [&](Rows& r, const Look& l) {
+    int v = l.e;
+    if constexpr (kPaged)
+      v = l.rel >= 0 && l.e >= 0 && l.e < a.num_blocks ? l.e * a.page_units + l.rel * a.row_units : -1;
     // the scale first: older than the rows, its wait comes free with theirs
-    r.sv = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(max(v, 0)) * a.skv + kLatent);
+    r.sv = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(max(v, 0)) * unit_bytes + kLatent);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
       const int kid = max(__shfl(v, 16 * u + c, 64), 0);
-      const uint4* rp = reinterpret_cast<const uint4*>(a.kv + static_cast<int64_t>(kid) * a.skv + kHalfLat * w);
+      const uint4* rp = reinterpret_cast<const uint4*>(a.kv + static_cast<int64_t>(kid) * unit_bytes + kHalfLat * w);
 #pragma unroll
       for (int i = 0; i < 4; i++) r.d[u][i] = rp[4 * i + g];
     }
     r.vmask = static_cast<uint32_t>(__ballot(lane < kTile && v >= 0));
   };
 
-  // One tile: convert + S^T + V to LDS, then the gathers two tiles on, then
-  // the exchange, softmax and PV.
-  auto tile = [&](int n, Rows& cur, int& idx_ahead) {
+  // One tile: convert + S^T + V to LDS, then the index of tile n + 4, the
+  // lookup of tile n + 3 and the gathers of tile n + 2, then the exchange,
+  // softmax and PV.  raw_s / look_s hold tile n + 2's index and lookup on
+  // entry (the slot of n's parity), raw_o / look_o tile n + 3's.
+  auto tile = [&](int n, Rows& cur, int& raw_s, int& raw_o, Look& look_s, Look& look_o) {
     f32x4 s_part[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -693,8 +751,9 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
     // (kept below the conversions: hoisted above them the loads would hold a
     // second tile's registers while the converted operands are still live)
     __builtin_amdgcn_sched_barrier(0);
-    issue_rows(cur, idx_ahead, n + 2);
-    idx_ahead = load_idx(n + 4);
+    raw_s = load_raw(n + 4);
+    look_o = lookup(raw_o, n + 3);
+    issue_rows(cur, look_s);
     __syncthreads();
 
     // Full scores: wave 0's partial + wave 1's, the same order in both waves.
@@ -754,17 +813,19 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
   // Tiles go in pairs (an odd count ends with a fully masked tile, which
   // changes nothing): no branch in the loop body.
   Rows ra, rb;
-  int ia = -1, ib = -1;   // index of tile n + 2 (n even: ia, odd: ib), then n + 4 after use
+  int r0 = -1, r1 = -1;                  // raw slots (even, odd tiles)
+  Look l0 = {-1, -1}, l1 = {-1, -1};     // lookup slots
   if (ntiles > 0) {
-    const int i0 = load_idx(0), i1 = load_idx(1);
-    ia = load_idx(2);
-    ib = load_idx(3);
-    issue_rows(ra, i0, 0);
-    issue_rows(rb, i1, 1);
+    const int i0 = load_raw(0), i1 = load_raw(1), i2 = load_raw(2);
+    r1 = load_raw(3);
+    const Look k0 = lookup(i0, 0), k1 = lookup(i1, 1);
+    l0 = lookup(i2, 2);
+    issue_rows(ra, k0);
+    issue_rows(rb, k1);
   }
   for (int n = 0; n < ntiles; n += 2) {
-    tile(n, ra, ia);
-    tile(n + 1, rb, ib);
+    tile(n, ra, r0, r1, l0, l1);
+    tile(n + 1, rb, r1, r0, l1, l0);
   }
 
   // Both waves hold the same m and l; each writes its latent half.
@@ -1071,15 +1132,18 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   const bool pipe = a.split_len > kChunkTiles * kTile;
   const int mode = a.pools != nullptr ? kPooledPos : a.bt != nullptr ? kPagedPos : kFlatRows;
 #define GLM53_LAUNCH(M, P) hipLaunchKernelGGL((sparse_mla_kernel<M, P>), grid, dim3(kThreads), 0, st, a)
+#define GLM53_PAIR(M) hipLaunchKernelGGL((sparse_mla_pair_kernel<M>), grid, dim3(128), 0, st, a)
+  // Long splits go to the pair kernel, whose masked keys read row 0 (page 0):
+  // it needs a non-empty cache (seq_kv counts rows, or pages when paged).
+  const bool pair = pipe && a.seq_kv > 0;
   if (mode == kPooledPos) {
-    if (pipe) GLM53_LAUNCH(kPooledPos, true); else GLM53_LAUNCH(kPooledPos, false);
+    if (pair) GLM53_PAIR(kPooledPos); else if (pipe) GLM53_LAUNCH(kPooledPos, true); else GLM53_LAUNCH(kPooledPos, false);
   } else if (mode == kPagedPos) {
-    if (pipe) GLM53_LAUNCH(kPagedPos, true); else GLM53_LAUNCH(kPagedPos, false);
-  } else if (pipe && a.seq_kv > 0) {   // (its masked keys read row 0)
-    hipLaunchKernelGGL((sparse_mla_pair_kernel<kFlatRows>), grid, dim3(128), 0, st, a);
+    if (pair) GLM53_PAIR(kPagedPos); else if (pipe) GLM53_LAUNCH(kPagedPos, true); else GLM53_LAUNCH(kPagedPos, false);
   } else {
-    if (pipe) GLM53_LAUNCH(kFlatRows, true); else GLM53_LAUNCH(kFlatRows, false);
+    if (pair) GLM53_PAIR(kFlatRows); else if (pipe) GLM53_LAUNCH(kFlatRows, true); else GLM53_LAUNCH(kFlatRows, false);
   }
+#undef GLM53_PAIR
 #undef GLM53_LAUNCH
 }
 
