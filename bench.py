@@ -41,6 +41,7 @@ for p in (str(ROOT), str(ROOT / "glm-5.3-kernels_amd")):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
+FP8_PEAK_FLOPS = 5.0e15   # MI355X dense FP8 matrix peak
 METRIC = "sparse-MLA decode µs/step + achieved HBM GB/s, B1/B8, 262k ctx, 2176 idx"
 
 
@@ -149,6 +150,9 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
         qpi, cpi, wpi, lpi, bpi, npi = W.indexer_prefill_inputs(dev, gi)
         fn = lambda: indexer_topk(fp8_paged_mqa_logits(qpi, cpi, wpi, lpi, bpi, npi, clean_logits=False), lpi,
                                   W.INDEX_TOPK_POOLS)
+        # rows share their keys: the logits' bound is the matrix cores, so
+        # report FLOP/s (the GB/s below counts each row's keys once per row)
+        log(f"case indexer_prefill: logits {W.indexer_flops(lpi) / 1e12:.3f} TFLOP per call")
         nbytes = W.indexer_bytes(lpi)
     else:   # decode_b8_split: the split kernel alone at the auto split count
         s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
@@ -597,8 +601,11 @@ def main():
         glo.replay()
         us_plo = timer.median_loop(glo, 2) / 3
         del glo
+        fl = W.indexer_flops(lpi)
         extra["indexer_prefill_2048_rows"] = {"ms_logits_plus_topk": round(us_pi / 1e3, 4),
                                               "ms_logits": round(us_plo / 1e3, 4),
+                                              "logits_fp8_tflops": round(fl / (us_plo * 1e-6) / 1e12, 1),
+                                              "logits_mfma_frac": round(fl / (us_plo * 1e-6) / FP8_PEAK_FLOPS, 3),
                                               "reference_ms_replicated_sm80": 20.632,
                                               "speedup_vs_reference": round(20.632e3 / us_pi, 1),
                                               "pools": npi, "rows": int(lpi.numel()), "heads": W.INDEX_HEADS}

@@ -22,7 +22,8 @@
 // v_mfma_scale_f32_16x16x128_f8f6f4 (unit scales) with A = q (16 heads x
 // 128 dims), B = k^T (128 dims x 16 keys).  Lane (g, c) of D holds key c for
 // heads 4g + [0, 4) of each head tile, so the relu-weighted head sum is 4
-// FMAs per tile and two cross-row swaps.  Each lane's B operand is dims
+// clamps and 4 FMAs per tile and two cross-row swaps, the key's scale one
+// multiply after the sum (relu(s d) = |s| relu(+-d)).  Each lane's B operand is dims
 // [16g, 16g + 16) and [64 + 16g, 64 + 16g + 16) of key c and the A operand
 // the same dims of its head: k-slot 32g + 8m + e is dim 16g + 8m + e
 // (m < 2), 64 + 16g + 8(m - 2) + e (m >= 2) on both sides, so each of the
@@ -82,6 +83,18 @@ __device__ __forceinline__ float row_sum4(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// The same sum for four values at once: on return lane (g, c) holds v[g]
+// summed over the four rows at column c.  Three swaps instead of eight, and
+// every addition in the order row_sum4 uses: (g0 + g2) + (g1 + g3).
+__device__ __forceinline__ float row_sum4x4(const float (&v)[4]) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[2]), false, false);
+  const float s02 = __uint_as_float(a[0]) + __uint_as_float(a[1]);   // lanes 0-31: v[0], 32-63: v[2]
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[1]), __float_as_uint(v[3]), false, false);
+  const float s13 = __uint_as_float(b[0]) + __uint_as_float(b[1]);   // lanes 0-31: v[1], 32-63: v[3]
+  const auto d = __builtin_amdgcn_permlane16_swap(__float_as_uint(s02), __float_as_uint(s13), false, false);
+  return __uint_as_float(d[0]) + __uint_as_float(d[1]);
+}
+
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // A lane's 32 bytes of a key (dims 16g + [0, 16) and 64 + 16g + [0, 16)) as
@@ -100,6 +113,26 @@ __device__ __forceinline__ f32x4v dot128_fp8(const uint64_t (&q)[4], const i32x8
   const f32x4v zero = {0.f, 0.f, 0.f, 0.f};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(qa, kb, zero, 0, 0, 0, 127, 0, 127);
 }
+
+// The key's scale taken out of the head sum: relu(s d) = |s| relu(d') with
+// d' = d for s >= 0 and d' = -d for s < 0 (the key's E4M3 sign bits
+// flipped, which negates its products exactly), so a (key, head) costs a
+// clamp and an FMA and the scale one multiply per key.  A NaN scale gives
+// 0, as fmax(NaN * d, 0) = 0 does for every head.
+__device__ __forceinline__ i32x8 signed_key(i32x8 kb, float sc) {
+  const int flip = sc < 0.f ? static_cast<int>(0x80808080u) : 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) kb[i] ^= flip;
+  return kb;
+}
+__device__ __forceinline__ float key_factor(float sc) { return sc != sc ? 0.f : fabsf(sc); }
+
+// relu of an unscaled product: v_med3_f32 clamps into [0, 3e38] (|q . k| <=
+// 128 * 448^2), and for a NaN input returns the minimum of the other two
+// (IEEE mode drops a quiet NaN), 0 -- the fmax(x, 0) semantics, in one
+// instruction: fmaxf itself would first quiet its input, since the compiler
+// cannot tell that a matrix-core result is never a signalling NaN.
+__device__ __forceinline__ float relu_dot(float d) { return __builtin_amdgcn_fmed3f(d, 0.f, 3.0e38f); }
 
 // Loads of one 16-key group (keys j0 + c) into registers: the 32 key bytes
 // of this lane (dims 32g + [0, 32)) and the key's scale.  blk is the page of
@@ -129,7 +162,8 @@ __device__ __forceinline__ void load_group(const LogitsArgs& a, int t, int j0, i
   // the cache), so the count of loads in flight is the same on all paths
   // and a wait for one group never drains the later groups' loads.
   const uint8_t* page = a.kv + static_cast<int64_t>(ok ? bj : 0) * a.page_bytes;
-  const int off = jb % a.block_size;
+  // aligned: j0 is uniform and the group within one page, so the division is scalar
+  const int off = kAligned ? j0 % a.block_size + (jb - j0) : jb % a.block_size;
   const uint4* kp = reinterpret_cast<const uint4*>(page + static_cast<int64_t>(off) * kHeadDim + 16 * g);
   gr.kd[0] = kp[0];   // dims 16g + [0, 16): with the other 3 lane groups, the key's first 64-byte half
   gr.kd[1] = kp[4];   // dims 64 + 16g + [0, 16): its second half
@@ -184,7 +218,6 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
 
   float* out = a.logits + t * a.sl_t;
   __shared__ float res[kLogitWaves][16 * kN];
-  __shared__ uint8_t put[kLogitWaves][16 * kN];   // 1: write res, 0: leave the position untouched
   Group ring[kDepth];
   // group i of the run, or past the run's end (a row's tail) its last group
   // again, loaded and not used
@@ -203,26 +236,23 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
       const Group& gr = ring[i % kDepth];
       const int j = j_wave + 16 * i + c;
       float v = 0.f;
-      const float sc = gr.kok ? gr.sc : 0.f;
       if (gr.live) {
         const uint64_t k0 = (static_cast<uint64_t>(gr.kd[0].y) << 32) | gr.kd[0].x;
         const uint64_t k1 = (static_cast<uint64_t>(gr.kd[0].w) << 32) | gr.kd[0].z;
         const uint64_t k2 = (static_cast<uint64_t>(gr.kd[1].y) << 32) | gr.kd[1].x;
         const uint64_t k3 = (static_cast<uint64_t>(gr.kd[1].w) << 32) | gr.kd[1].z;
-        const i32x8 kb = key_operand(k0, k1, k2, k3);
+        const i32x8 kb = signed_key(key_operand(k0, k1, k2, k3), gr.sc);
 #pragma unroll
         for (int ht = 0; ht < kTiles; ht++) {
           const f32x4v d = dot128_fp8(qf[ht], kb);
 #pragma unroll
-          for (int e = 0; e < 4; e++) v = __builtin_fmaf(wv[ht][e], fmaxf(sc * d[e], 0.f), v);
+          for (int e = 0; e < 4; e++) v = __builtin_fmaf(wv[ht][e], relu_dot(d[e]), v);
         }
-        v = row_sum4(v);
+        v = key_factor(gr.sc) * row_sum4(v);
       }
-      if (g == 0) {
-        // page outside the cache, or past the context: -inf (past the context only when cleaning)
-        res[w][16 * i + c] = gr.kok ? v : -__builtin_inff();
-        put[w][16 * i + c] = j < j_end && (gr.kok || j < len || a.clean);
-      }
+      // page outside the cache, or past the context: -inf (written past the
+      // context only when cleaning, which the stores below decide)
+      if (g == 0) res[w][16 * i + c] = gr.kok ? v : -__builtin_inff();
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -231,7 +261,8 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
 #pragma unroll
   for (int r = 0; r < (16 * kN + 63) / 64; r++) {
     const int idx = 64 * r + lane;
-    if (idx < 16 * n && put[w][idx]) out[j_wave + idx] = res[w][idx];
+    const int j = j_wave + idx;   // written inside the run, and past the context only when cleaning
+    if (idx < 16 * n && j < j_end && (j < len || a.clean)) out[j] = res[w][idx];
   }
 }
 
@@ -245,7 +276,7 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
 // kernel above; block sizes that are a multiple of 16 only.
 template <int kTiles, int kN>
 __global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(const LogitsArgs a, int num_tokens) {
-  constexpr int kR = 4;        // rows per wave
+  constexpr int kR = 4;        // rows per wave (row_sum4x4 leaves row g's sums in lane group g)
   constexpr int kDepth = 4;
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
@@ -264,6 +295,7 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(cons
     len[r] = l;
     len_max = len_max > l ? len_max : l;
   }
+  const int my_len = g == 0 ? len[0] : g == 1 ? len[1] : g == 2 ? len[2] : len[3];   // row 4w + g
 
   // page of each group's first key (lane i < n: group i; -1 past every row's context)
   int blk_l = -1;
@@ -292,7 +324,6 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(cons
   }
 
   __shared__ float res[kLogitWaves][kR][16 * kN];
-  __shared__ uint8_t put[kLogitWaves][kR][16 * kN];   // 1: write res, 0: leave the position untouched
   Group ring[kDepth];
   // group i of the run, or past the run's end its last group again (loaded, not used)
   auto load = [&](int i, Group& gr) {
@@ -309,34 +340,28 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(cons
       if (i >= n) continue;   // uniform (the tail of the rows)
       const Group& gr = ring[i % kDepth];
       const int j = j_run + 16 * i + c;
-      float v[kR] = {};
+      float tot = 0.f;   // lane (g, c): row 4w + g at key j
       if (gr.live) {
         const uint64_t k0 = (static_cast<uint64_t>(gr.kd[0].y) << 32) | gr.kd[0].x;
         const uint64_t k1 = (static_cast<uint64_t>(gr.kd[0].w) << 32) | gr.kd[0].z;
         const uint64_t k2 = (static_cast<uint64_t>(gr.kd[1].y) << 32) | gr.kd[1].x;
         const uint64_t k3 = (static_cast<uint64_t>(gr.kd[1].w) << 32) | gr.kd[1].z;
-        const i32x8 kb = key_operand(k0, k1, k2, k3);
+        const i32x8 kb = signed_key(key_operand(k0, k1, k2, k3), gr.sc);
+        float v[kR] = {};
 #pragma unroll
         for (int r = 0; r < kR; r++) {
-          const float sc = gr.kok && j < len[r] ? gr.sc : 0.f;
 #pragma unroll
           for (int ht = 0; ht < kTiles; ht++) {
             const f32x4v d = dot128_fp8(qf[r][ht], kb);
 #pragma unroll
-            for (int e = 0; e < 4; e++) v[r] = __builtin_fmaf(wv[r][ht][e], fmaxf(sc * d[e], 0.f), v[r]);
+            for (int e = 0; e < 4; e++) v[r] = __builtin_fmaf(wv[r][ht][e], relu_dot(d[e]), v[r]);
           }
-          v[r] = row_sum4(v[r]);
         }
+        tot = key_factor(gr.sc) * row_sum4x4(v);
       }
-      if (g == 0) {
-#pragma unroll
-        for (int r = 0; r < kR; r++) {
-          const bool ok = gr.kok && j < len[r];
-          // page outside the cache, or past the row's context: -inf (past the context only when cleaning)
-          res[w][r][16 * i + c] = ok ? v[r] : -__builtin_inff();
-          put[w][r][16 * i + c] = j < j_end && (j < len[r] || a.clean);
-        }
-      }
+      // page outside the cache, or past the row's context: -inf (written past
+      // the context only when cleaning, which the stores below decide)
+      res[w][g][16 * i + c] = gr.kok && j < my_len ? tot : -__builtin_inff();
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -349,7 +374,8 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(cons
 #pragma unroll
     for (int q = 0; q < (16 * kN + 63) / 64; q++) {
       const int idx = 64 * q + lane;
-      if (idx < 16 * n && put[w][r][idx]) out[j_run + idx] = res[w][r][idx];
+      const int j = j_run + idx;   // written inside the run, and past the row's context only when cleaning
+      if (idx < 16 * n && j < j_end && (j < len[r] || a.clean)) out[j] = res[w][r][idx];
     }
   }
 }
@@ -820,8 +846,8 @@ extern "C" int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t s
   // group when groups straddle pages (block_size % 16 != 0).
   const bool al = block_size % 16 == 0;
   if (bt_stride == 0 && al && num_tokens >= 16) {
-    // one table shared by every row (a request's prefill chunk): 16 rows per workgroup
-    constexpr int kRowsN = 16;
+    // one table shared by every row (a request's prefill chunk): 16 rows x 512 keys per workgroup
+    constexpr int kRowsN = 32;
     LogitsArgs a{static_cast<const uint8_t*>(q), sq_t, sq_h, static_cast<const uint8_t*>(kv_cache), page_bytes,
                  static_cast<int>(block_size), static_cast<int>(num_blocks), weights, sw_t, context_lens,
                  block_table, 0, static_cast<int>(max_blocks), static_cast<int>(num_heads),

@@ -257,6 +257,39 @@ def test_logits_nan_codes(cuda, oracle):
     assert np.array_equal(top.cpu().numpy(), oracle.indexer_topk(g0.numpy(), lens.cpu().numpy(), 512))
 
 
+def test_logits_negative_and_zero_scales(cuda, oracle):
+    """Keys with negative, -0.0 and +0.0 scales (the writer only makes
+    positive ones): relu(s q.k) for s < 0 keeps the keys whose product is
+    negative, which the kernels get by flipping the key's E4M3 sign bits and
+    scaling by |s|; zero scales give 0.  Both logits kernels (per-token rows
+    and rows sharing one table) against the oracle, and bit-identical to
+    each other."""
+    import torch
+    from sparse_indexer import fp8_paged_mqa_logits
+    g = torch.Generator(device=cuda).manual_seed(41)
+    bs, pools, T = 64, 1536, 20
+    cache, nb = W.indexer_cache(cuda, g, pools, bs)
+    pages = torch.as_strided(cache, (nb, cache.stride(0)), (cache.stride(0), 1))
+    sc = pages[:, bs * 128: bs * 132].contiguous().view(torch.float32)        # [nb, bs] scales
+    flip = torch.rand(sc.shape, generator=g, device=cuda) < 0.3
+    sc = torch.where(flip, -sc, sc)
+    sc[0, 3], sc[1, 7], sc[2, 0] = -0.0, 0.0, -sc[2, 0].abs()
+    pages[:, bs * 128: bs * 132] = sc.view(torch.uint8)
+    qf = torch.randn(T, 1, 32, 128, generator=g, device=cuda)
+    q = (qf * (448.0 / qf.abs().amax(dim=-1, keepdim=True))).to(torch.float8_e4m3fn)
+    w = (torch.randn(T, 32, generator=g, device=cuda) / 32 ** 0.5).contiguous()
+    lens = torch.randint(pools // 2, pools + 1, (T,), generator=g, device=cuda, dtype=torch.int32)
+    table = torch.arange(nb, device=cuda, dtype=torch.int32)
+    shared = table[None, :].expand(T, nb)
+    log_case("indexer logits with negative and zero scales")
+    got = fp8_paged_mqa_logits(q, cache, w, lens, shared, pools)
+    per_row = fp8_paged_mqa_logits(q, cache, w, lens, shared.contiguous(), pools)
+    torch.cuda.synchronize()
+    assert torch.equal(got, per_row)
+    check_logits(oracle, got, q, cache, w, lens, shared.contiguous(), pools, True)
+    assert got[:, 3].eq(0).all() and got[:, 64 + 7].eq(0).all()
+
+
 def test_logits_random_shapes(cuda, oracle):
     """Seeded random batch, next_n, heads, block sizes (straddling and not),
     page padding, contexts, table entries outside the cache, clean or not."""

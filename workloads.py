@@ -290,6 +290,12 @@ def indexer_bytes(lens: torch.Tensor, heads=INDEX_HEADS) -> int:
     return n * (INDEX_DIM + 4) + t * heads * (INDEX_DIM + 4) + n * 4
 
 
+def indexer_flops(lens: torch.Tensor, heads=INDEX_HEADS) -> int:
+    """FP8 multiply-adds of the logits as FLOPs: 2 * 128 per (valid pool
+    key, head) of each query row."""
+    return 2 * INDEX_DIM * heads * int(lens.clamp(min=0).sum().item())
+
+
 # ----------------------------------------------------------------- bytes
 
 def writer_bytes(n_rows: int) -> int:
