@@ -70,24 +70,24 @@ def _choose_num_kv_splits_mi355x(num_tokens: int, num_head_groups: int, index_to
     The split kernel runs one 512-thread workgroup per (split, token, head
     group) and needs ~106 KB of LDS, so one workgroup fits a compute unit.
     Decode latency is set by the per-workgroup chain (index load -> row
-    gather -> tiles), so the top-k axis is cut into as many whole 32-key
-    tiles per split as still lets every workgroup start in the first wave
-    and gives each of the workgroup's two key groups a tile: the largest
-    divisor of topk / 32 with tokens * groups * splits <= CUs and at least
-    two tiles per split (B=1 at 2176 indices: 34 splits, 10.47 us against
-    10.67 us with 68 one-tile splits).  (The reference's
-    _choose_num_kv_splits targets Triton on 70 SMs and is kept above,
-    unchanged, for callers that want its exact answers.)
+    gather -> tiles), so the split count is capped where every workgroup
+    still starts in the first wave (tokens * groups * splits <= CUs) and
+    each of the workgroup's two key groups gets a tile (two 32-key tiles per
+    split); under that cap it takes the fewest tiles per split, then the
+    fewest splits that give that many (fewer split partials for the merge).
+    B=1, 2, 4 at 2176 indices: 34 splits of 2 tiles; B=8: 23 splits of 3
+    (13.2 us per step over a 5-layer rotation against 13.4 us for the 17
+    splits of 4 tiles that a divisor of the tile count would give).  (The
+    reference's _choose_num_kv_splits targets Triton on 70 SMs and is kept
+    above, unchanged, for callers that want its exact answers.)
     """
     base = num_tokens * num_head_groups
     if base == 0 or index_topk % _MIN_BLOCK_N:
         return 1
     tiles = index_topk // _MIN_BLOCK_N
-    best = 1
-    for d in range(1, tiles // 2 + 1):
-        if tiles % d == 0 and base * d <= cu_count:
-            best = d
-    return best
+    cap = max(1, min(cu_count // base, tiles // 2))
+    per_split = -(-tiles // cap)
+    return -(-tiles // per_split)
 
 
 def triton_mla_sparse_attention(
