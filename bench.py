@@ -97,6 +97,15 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def split_kernel_threads(topk: int, splits: int) -> int:
+    """Threads per workgroup of the decode split kernel the library launches
+    for this split length: 12 waves (three key groups) for splits of 65-96
+    keys, 8 waves otherwise (splits past 256 keys take the 2-wave pair
+    kernel, which the decode workloads never reach)."""
+    split_len = -(-topk // splits)
+    return 768 if 64 < split_len <= 96 else 512
+
+
 def capture(torch, fn, unroll: int = 1):
     fn()
     torch.cuda.synchronize()
@@ -715,7 +724,7 @@ def main():
     # and says so.
     ach = bytes8 / (us8_kernel * 1e-6) / 1e9
     traffic, traffic_note = None, None
-    key = f"sparse_mla_kernel@{s8 * 8 * 512}"
+    key = f"sparse_mla_kernel@{s8 * 8 * split_kernel_threads(W.TOPK, s8)}"
     tf = ROOT / "profiles" / "hbm_bytes_per_dispatch.json"
     d = json.loads(tf.read_text())["per_dispatch"].get(key) if tf.exists() else None
     if d:

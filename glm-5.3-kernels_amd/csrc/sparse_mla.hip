@@ -16,6 +16,9 @@
 //     key group w / 4 (even / odd tiles), each key group running its own
 //     online softmax; the two are merged through LDS at the end.  Two waves
 //     per SIMD interleave their tiles, hiding each other's latencies.
+//     Splits of exactly three tiles (65-96 keys: B=8's 23 splits) take a
+//     12-wave variant, 3 key groups x 4 slices, that consumes them in one
+//     round instead of two (the second with one group idle).
 //   * Lane (g = lane / 16, c = lane % 16) gathers 32 bytes of its wave's
 //     slice from keys c and 16 + c of a tile: four 16-byte loads per tile,
 //     slice bytes 16g + [0, 16) and 64 + 16g + [0, 16), so each load
@@ -143,16 +146,31 @@ __device__ __forceinline__ void i8x16_to_bf16(const uint4 v, bf16x8& lo, bf16x8&
   hi = __builtin_bit_cast(bf16x8, b);
 }
 
+// Shape of the split kernel for kG key groups of kSlices waves: two groups
+// take chunks of 8 tiles in 4 rounds (any decode split); three take one
+// round of 3 tiles (splits of at most 96 keys: B=8's 23 splits of 95 keys
+// in one round instead of two).
+template <int kG>
+struct SplitShape {
+  static constexpr int kWaves = kSlices * kG;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kChunkTiles = kG == 2 ? 8 : kG;
+  static constexpr int kRounds = kChunkTiles / kG;
+  static constexpr int kRedBufs = kRounds > 1 ? 2 : 1;   // partial S^T double-buffered across rounds
+};
+
+template <int kG>
 struct __attribute__((aligned(16))) MlaShared {
+  using S = SplitShape<kG>;
   union {
-    uint16_t vbuf[kWaves][kTile][kVStride];          // per-wave bf16 V slice of a tile
+    uint16_t vbuf[S::kWaves][kTile][kVStride];       // per-wave bf16 V slice of a tile
     struct {
-      float rows[kGroups][kHeads][kRowStride];         // each key group's acc, row-major
-      float ml[kGroups][kHeads][2];                    // each key group's (m, l) per head
+      float rows[kG][kHeads][kRowStride];              // each key group's acc, row-major
+      float ml[kG][kHeads][2];                         // each key group's (m, l) per head
     } fin;
   };
-  float4 red[2][kGroups][kSlices][2][64];              // partial S^T per slice: [half][lane]
-  float scl[2][kChunkTiles][kTile];                    // row scales of the chunk
+  float4 red[S::kRedBufs][kG][kSlices][2][64];         // partial S^T per slice: [half][lane]
+  float scl[2][S::kChunkTiles][kTile];                 // row scales of the chunk
 };
 
 // Request-relative token position -> flat cache row, the conversion vLLM's
@@ -218,15 +236,21 @@ __device__ __forceinline__ int pooled_position(PoolAt pool, int num_pools, int p
 // banks; the 16-byte chunks of rows 8-15 of every 16 (row bit 3) are XOR-
 // swapped in pairs so that a 16-byte write of 16 consecutive rows at one
 // column is conflict-free too (without it rows r and r + 8 share banks).
-__device__ __forceinline__ uint16_t* vbuf_at(MlaShared& sh, int w, int row, int col) {
+template <class Shared>
+__device__ __forceinline__ uint16_t* vbuf_at(Shared& sh, int w, int row, int col) {
   const int chunk = (col >> 3) ^ ((row >> 3) & 1);
   return &sh.vbuf[w][row][(chunk << 3) | (col & 7)];
 }
 
-template <int kMode, bool kPipe>
-__global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
+template <int kMode, bool kPipe, int kG>
+__global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(const MlaArgs a) {
   constexpr bool kPaged = kMode != kFlatRows;
-  __shared__ MlaShared sh;
+  constexpr int kWaves = SplitShape<kG>::kWaves;
+  constexpr int kChunkTiles = SplitShape<kG>::kChunkTiles;
+  constexpr int kRounds = SplitShape<kG>::kRounds;
+  constexpr int kRedBufs = SplitShape<kG>::kRedBufs;
+  static_assert(kG == 2 || !kPipe, "three key groups take single-chunk splits only");
+  __shared__ MlaShared<kG> sh;
 
   // Workgroups go to the 8 XCDs round robin by linear id; numbering the
   // (token, head group) units fastest puts all splits of a unit on one XCD
@@ -294,7 +318,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
   auto load_ids = [&](int c0, int (&id)[kRounds]) {
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
-      const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
+      const int pos = c0 + (kG * r + kg) * kTile + (lane & 31);
       int v;
       if (kMode == kPooledPos)
         v = pos < end ? pooled_position([&](int j) { return pools_t[j]; }, a.num_pools, a.pool_size,
@@ -311,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
                         uint32_t (&vmask)[kRounds]) {
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
-      const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
+      const int pos = c0 + (kG * r + kg) * kTile + (lane & 31);
       int v = pos < end ? raw[r] : -1;
       if (kPaged)
         v = to_page_unit(bt_req, max_blocks, a.block_size, a.num_blocks, a.page_units, a.row_units, v);
@@ -354,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
     }
     if (sl == 0 && lane < kTile) {
 #pragma unroll
-      for (int r = 0; r < kRounds; r++) sh.scl[cbuf][2 * r + kg][lane] = svc[r];
+      for (int r = 0; r < kRounds; r++) sh.scl[cbuf][kG * r + kg][lane] = svc[r];
     }
     if (kPipe) load_ids(c1, idn);
 
@@ -362,8 +386,8 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
 #pragma unroll
     for (int r = 0; r < kRounds; r++, buf ^= 1) {
       if (kPipe && r == kRounds / 2) issue_rows(c1, idn, kdn, svn, vmn);   // next chunk's rows (-1 past the split)
-      if (c0 + 2 * r * kTile >= end) continue;                   // uniform across the workgroup
-      const bool has_tile = c0 + (2 * r + kg) * kTile < end;     // uniform across the wave
+      if (c0 + kG * r * kTile >= end) continue;                  // uniform across the workgroup
+      const bool has_tile = c0 + (kG * r + kg) * kTile < end;    // uniform across the wave
       uint4 (&kd)[kRounds][2][2] = kdc;
       uint32_t (&vmask)[kRounds] = vmc;
 
@@ -387,13 +411,13 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
           *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 64 + 16 * g)) = __builtin_bit_cast(uint4, k45);
           *reinterpret_cast<uint4*>(vbuf_at(sh, w, vrow, 64 + 16 * g + 8)) = __builtin_bit_cast(uint4, k67);
         }
-        sh.red[buf][kg][sl][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
-        sh.red[buf][kg][sl][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
+        sh.red[buf % kRedBufs][kg][sl][0][lane] = make_float4(s_part[0][0], s_part[0][1], s_part[0][2], s_part[0][3]);
+        sh.red[buf % kRedBufs][kg][sl][1][lane] = make_float4(s_part[1][0], s_part[1][1], s_part[1][2], s_part[1][3]);
       }
       __syncthreads();
       if (!has_tile) continue;
 
-      const int tile = 2 * r + kg;
+      const int tile = kG * r + kg;
       const float4 sc0 = *reinterpret_cast<const float4*>(&sh.scl[cbuf][tile][4 * g]);
       const float4 sc1 = *reinterpret_cast<const float4*>(&sh.scl[cbuf][tile][16 + 4 * g]);
       const float sc[8] = {sc0.x, sc0.y, sc0.z, sc0.w, sc1.x, sc1.y, sc1.z, sc1.w};
@@ -405,8 +429,8 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
         float4 rr[kSlices][2];
 #pragma unroll
         for (int ss = 0; ss < kSlices; ss++) {
-          rr[ss][0] = sh.red[buf][kg][ss][0][lane];
-          rr[ss][1] = sh.red[buf][kg][ss][1][lane];
+          rr[ss][0] = sh.red[buf % kRedBufs][kg][ss][0][lane];
+          rr[ss][1] = sh.red[buf % kRedBufs][kg][ss][1][lane];
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -478,7 +502,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
     }
   }
 
-  // ---- combine the two key groups and write the 16 result rows.  The MFMA
+  // ---- combine the key groups and write the 16 result rows.  The MFMA
   // C layout scatters a lane's values over 16 rows (16 x 64-byte pieces per
   // store instruction, which the memory pipeline issues ~2.5x slower than
   // contiguous ones), so both key groups park their accumulators row-major
@@ -496,27 +520,41 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_kernel(const MlaArgs a) {
     }
   }
   __syncthreads();
+  constexpr int kRowsPerWave = (kHeads + kWaves - 1) / kWaves;
 #pragma unroll
-  for (int k = 0; k < kHeads / kWaves; k++) {
-    const int r = (kHeads / kWaves) * w + k;   // result row (head in the group), uniform per wave
+  for (int k = 0; k < kRowsPerWave; k++) {
+    // result row (head in the group), uniform per wave: consecutive rows per
+    // wave when they divide evenly, else dealt round robin
+    const int r = kHeads % kWaves == 0 ? kRowsPerWave * w + k : w + kWaves * k;
     const int hd = hg * kHeads + r;
-    if (hd >= a.num_heads) break;
-    const float m0 = sh.fin.ml[0][r][0], l0 = sh.fin.ml[0][r][1];
-    const float m1 = sh.fin.ml[1][r][0], l1 = sh.fin.ml[1][r][1];
-    const float mm = fmaxf(m0, m1);
-    const float a0 = fast_exp2(m0 - mm);
-    const float a1 = fast_exp2(m1 - mm);
-    const float l = l0 * a0 + l1 * a1;
+    if (r >= kHeads || hd >= a.num_heads) break;
+    float mg[kG], ag[kG];
+    float mm = kNegLarge;
+#pragma unroll
+    for (int i = 0; i < kG; i++) {
+      mg[i] = sh.fin.ml[i][r][0];
+      mm = i == 0 ? mg[0] : fmaxf(mm, mg[i]);
+    }
+    float l = 0.f;
+#pragma unroll
+    for (int i = 0; i < kG; i++) {
+      ag[i] = fast_exp2(mg[i] - mm);
+      const float li = sh.fin.ml[i][r][1] * ag[i];
+      l = i == 0 ? li : l + li;
+    }
     // 1 / l once, then multiplies (the reference divides; the two differ by
     // at most one fp32 ulp before the bf16 / fp32 store).
     const float inv_l = 1.f / (l > 0.f ? l : 1.f);
-    const float* r0 = sh.fin.rows[0][r];
-    const float* r1 = sh.fin.rows[1][r];
+    // key groups added in order: (x0 a0 + x1 a1) + x2 a2
     auto fin4 = [&](int col) {
-      const float4 x0 = *reinterpret_cast<const float4*>(r0 + col);
-      const float4 x1 = *reinterpret_cast<const float4*>(r1 + col);
-      return make_float4((x0.x * a0 + x1.x * a1) * inv_l, (x0.y * a0 + x1.y * a1) * inv_l,
-                         (x0.z * a0 + x1.z * a1) * inv_l, (x0.w * a0 + x1.w * a1) * inv_l);
+      float4 v = *reinterpret_cast<const float4*>(&sh.fin.rows[0][r][col]);
+      v = make_float4(v.x * ag[0], v.y * ag[0], v.z * ag[0], v.w * ag[0]);
+#pragma unroll
+      for (int i = 1; i < kG; i++) {
+        const float4 x = *reinterpret_cast<const float4*>(&sh.fin.rows[i][r][col]);
+        v = make_float4(v.x + x.x * ag[i], v.y + x.y * ag[i], v.z + x.z * ag[i], v.w + x.w * ag[i]);
+      }
+      return make_float4(v.x * inv_l, v.y * inv_l, v.z * inv_l, v.w * inv_l);
     };
     if (a.num_splits == 1 && !a.partials_only) {
       // lane: latents [8 lane, 8 lane + 8) -> one 16-byte bf16 store
@@ -611,11 +649,11 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
   // maps every key to -1.
   const int req = kPaged ? a.req_id[t] : 0;
   const bool req_ok = kPaged && req >= 0 && req < a.num_reqs && a.max_blocks > 0;
-  const int32_t* bt_req = req_ok ? a.bt + static_cast<int64_t>(req) * a.bt_stride : a.req_id + t;
+  const int32_t* bt_req = !kPaged ? nullptr : req_ok ? a.bt + static_cast<int64_t>(req) * a.bt_stride : a.req_id + t;
   const int max_blocks = req_ok ? a.max_blocks : 0;
   const int last_blk = max(max_blocks, 1) - 1;
   // Pooled mode: the token's pool ids (with none, req_id[t] stands in and is never used)
-  const int32_t* pools_t = kMode == kPooledPos && a.num_pools > 0 ? a.pools + t * a.sp_t : a.req_id + t;
+  const int32_t* pools_t = kMode != kPooledPos ? nullptr : a.num_pools > 0 ? a.pools + t * a.sp_t : a.req_id + t;
   const int last_pool = max(a.num_pools, 1) - 1;
   const int seq_len_t = kMode == kPooledPos && a.seq_lens ? a.seq_lens[t] : -1;
   uint8_t* vb = reinterpret_cast<uint8_t*>(&sh.vbuf[w][0][0]);
@@ -855,7 +893,11 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
 // them (the loaded bytes are folded with XOR so that no load is dead).  Its
 // duration is the floor that the split kernel's conversions, products and
 // softmax add to.
-__global__ __launch_bounds__(kThreads) void sparse_mla_gather_floor_kernel(const MlaArgs a) {
+template <int kG>
+__global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_floor_kernel(const MlaArgs a) {
+  constexpr int kWaves = SplitShape<kG>::kWaves;
+  constexpr int kChunkTiles = SplitShape<kG>::kChunkTiles;
+  constexpr int kRounds = SplitShape<kG>::kRounds;
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
   if ((gridDim.y * gridDim.z) % 8 == 0) {
     const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
@@ -883,7 +925,7 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_gather_floor_kernel(const
   for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile) {
 #pragma unroll
     for (int r = 0; r < kRounds; r++) {
-      const int pos = c0 + (2 * r + kg) * kTile + (lane & 31);
+      const int pos = c0 + (kG * r + kg) * kTile + (lane & 31);
       int v = pos < end ? idx_t[pos] : -1;
       if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv) v = -1;
 #pragma unroll
@@ -901,11 +943,12 @@ __global__ __launch_bounds__(kThreads) void sparse_mla_gather_floor_kernel(const
   }
   // a finite float from the folded bits, stored where the split kernel stores
   const float x = static_cast<float>(fold & 0xffff);
+  constexpr int kRowsPerWave = (kHeads + kWaves - 1) / kWaves;
 #pragma unroll
-  for (int k = 0; k < kHeads / kWaves; k++) {
-    const int r = (kHeads / kWaves) * w + k;
+  for (int k = 0; k < kRowsPerWave; k++) {
+    const int r = kHeads % kWaves == 0 ? kRowsPerWave * w + k : w + kWaves * k;   // as the split kernel
     const int hd = hg * kHeads + r;
-    if (hd >= a.num_heads) break;
+    if (r >= kHeads || hd >= a.num_heads) break;
     const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + hd;
     float* pp = a.part + row * kLatent;
     *reinterpret_cast<float4*>(pp + 4 * lane) = make_float4(x, x, x, x);
@@ -1131,18 +1174,26 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   // Splits longer than one chunk of gathers pipeline their chunks.
   const bool pipe = a.split_len > kChunkTiles * kTile;
   const int mode = a.pools != nullptr ? kPooledPos : a.bt != nullptr ? kPagedPos : kFlatRows;
-#define GLM53_LAUNCH(M, P) hipLaunchKernelGGL((sparse_mla_kernel<M, P>), grid, dim3(kThreads), 0, st, a)
+#define GLM53_LAUNCH(M, P) hipLaunchKernelGGL((sparse_mla_kernel<M, P, 2>), grid, dim3(kThreads), 0, st, a)
 #define GLM53_PAIR(M) hipLaunchKernelGGL((sparse_mla_pair_kernel<M>), grid, dim3(128), 0, st, a)
   // Long splits go to the pair kernel, whose masked keys read row 0 (page 0):
   // it needs a non-empty cache (seq_kv counts rows, or pages when paged).
   const bool pair = pipe && a.seq_kv > 0;
+  // Splits of exactly three tiles (65 to 96 keys) run in one round on three key groups.
+  const bool three = a.split_len > 2 * kTile && a.split_len <= 3 * kTile;
+#define GLM53_THREE(M) hipLaunchKernelGGL((sparse_mla_kernel<M, false, 3>), grid, \
+                                          dim3(SplitShape<3>::kThreads), 0, st, a)
   if (mode == kPooledPos) {
-    if (pair) GLM53_PAIR(kPooledPos); else if (pipe) GLM53_LAUNCH(kPooledPos, true); else GLM53_LAUNCH(kPooledPos, false);
+    if (pair) GLM53_PAIR(kPooledPos); else if (pipe) GLM53_LAUNCH(kPooledPos, true);
+    else if (three) GLM53_THREE(kPooledPos); else GLM53_LAUNCH(kPooledPos, false);
   } else if (mode == kPagedPos) {
-    if (pair) GLM53_PAIR(kPagedPos); else if (pipe) GLM53_LAUNCH(kPagedPos, true); else GLM53_LAUNCH(kPagedPos, false);
+    if (pair) GLM53_PAIR(kPagedPos); else if (pipe) GLM53_LAUNCH(kPagedPos, true);
+    else if (three) GLM53_THREE(kPagedPos); else GLM53_LAUNCH(kPagedPos, false);
   } else {
-    if (pair) GLM53_PAIR(kFlatRows); else if (pipe) GLM53_LAUNCH(kFlatRows, true); else GLM53_LAUNCH(kFlatRows, false);
+    if (pair) GLM53_PAIR(kFlatRows); else if (pipe) GLM53_LAUNCH(kFlatRows, true);
+    else if (three) GLM53_THREE(kFlatRows); else GLM53_LAUNCH(kFlatRows, false);
   }
+#undef GLM53_THREE
 #undef GLM53_PAIR
 #undef GLM53_LAUNCH
 }
@@ -1450,7 +1501,12 @@ extern "C" int glm53_sparse_mla_gather_floor(const void* q, int64_t sq_t, int64_
   const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
                   static_cast<unsigned>(a.heads_padded / kHeads));
   (void)hipGetLastError();
-  hipLaunchKernelGGL(sparse_mla_gather_floor_kernel, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  // the split kernel's workgroup shape for this split length (three key groups for 3-tile splits)
+  if (a.split_len > 2 * kTile && a.split_len <= 3 * kTile)
+    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<3>, grid, dim3(SplitShape<3>::kThreads), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else
+    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<2>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -38,6 +38,14 @@ def u16(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
+def kernel_groups(topk, splits):
+    """Online-softmax streams per split in the HIP kernel for this split
+    length: one (the pair kernel) past a chunk of 256 keys, three key groups
+    for splits of exactly three 32-key tiles, two otherwise."""
+    split_len = -(-topk // splits)
+    return 1 if split_len > 256 else 3 if 64 < split_len <= 96 else GROUPS
+
+
 def rows_np(cache):
     return cache.contiguous().view(torch.uint8).cpu().numpy().reshape(-1, 528)
 
@@ -110,7 +118,8 @@ def test_small_b1_splits(cuda, oracle, small_cache, splits):
     out = triton_mla_sparse_attention(w["q"], w["cache"].view(n, 1, 528), w["idx"], W.SM_SCALE,
                                       num_kv_splits=splits)
     torch.cuda.synchronize()
-    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
+    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=splits,
+                             groups=kernel_groups(w["idx"].shape[-1], splits), block_n=BLOCK, lazy=LAZY)
     mx, mean = compare(out, want, f"splits={splits}")
     assert mean < 1e-4        # ~bf16 ulp-level agreement
 
@@ -123,7 +132,8 @@ def test_small_auto_splits_and_graph(cuda, oracle, small_cache):
     kv = w["cache"].view(n, 1, 528)
     out = triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE)
     s = _choose_num_kv_splits_mi355x(1, 1, 2176, torch.cuda.get_device_properties(0).multi_processor_count)
-    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=s, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
+    want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=s,
+                             groups=kernel_groups(w["idx"].shape[-1], s), block_n=BLOCK, lazy=LAZY)
     compare(out, want, "auto")
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -203,7 +213,8 @@ def test_head_counts_and_edges(cuda, oracle, small_cache):
         idx = torch.randint(-50, n + 50, (3, 1, topk), generator=g, device=cuda, dtype=torch.int32)
         out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
         torch.cuda.synchronize()
-        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits,
+                                 groups=kernel_groups(idx.shape[-1], splits), block_n=BLOCK, lazy=LAZY)
         compare(out, want, (heads, topk, splits))
     # int64 indices, including values that alias valid rows modulo 2^32
     q = torch.randn(2, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
@@ -211,7 +222,8 @@ def test_head_counts_and_edges(cuda, oracle, small_cache):
     idx64[0, 0, :40] += 1 << 32
     out = triton_mla_sparse_attention(q, kv, idx64, W.SM_SCALE, num_kv_splits=2)
     clean = torch.where((idx64 >= 0) & (idx64 < n), idx64, -1).to(torch.int32)
-    want = oracle.sparse_mla(u16(q), rows, clean.cpu().numpy(), W.SM_SCALE, n_splits=2, groups=GROUPS, block_n=BLOCK, lazy=LAZY)
+    want = oracle.sparse_mla(u16(q), rows, clean.cpu().numpy(), W.SM_SCALE, n_splits=2,
+                             groups=kernel_groups(clean.shape[-1], 2), block_n=BLOCK, lazy=LAZY)
     compare(out, want, "int64")
     # no tokens
     empty = triton_mla_sparse_attention(q[:0], kv, idx64[:0].to(torch.int32), W.SM_SCALE)
@@ -243,7 +255,8 @@ def test_random_shapes(cuda, oracle, small_cache):
         log_case("mla random", case, T, heads, topk, splits, eff)
         out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits or None, sm_count=256)
         torch.cuda.synchronize()
-        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=eff, groups=GROUPS,
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=eff,
+                                 groups=kernel_groups(idx.shape[-1], eff),
                                  block_n=BLOCK, lazy=LAZY)
         compare(out, want, ("random", case, T, heads, topk, eff))
 
@@ -267,8 +280,8 @@ def test_xcd_grouped_units(cuda, oracle, small_cache):
         log_case("mla xcd-grouped", T, heads, topk, splits)
         out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
         torch.cuda.synchronize()
-        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=GROUPS,
-                                 block_n=BLOCK, lazy=LAZY)
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits,
+                                 groups=kernel_groups(idx.shape[-1], splits), block_n=BLOCK, lazy=LAZY)
         compare(out, want, ("xcd-grouped", T, heads, topk, splits))
 
 
@@ -299,7 +312,8 @@ def test_full_context_b1_b8(cuda, oracle, full_cache):
             torch.cuda.synchronize()
             s = splits or _choose_num_kv_splits_mi355x(q.shape[0], 1, 2176, cu)
             want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s,
-                                     nthreads=oracle.default_threads(), groups=GROUPS, block_n=BLOCK, lazy=LAZY)
+                                     nthreads=oracle.default_threads(), groups=kernel_groups(idx.shape[-1], s),
+                                     block_n=BLOCK, lazy=LAZY)
             compare(out, want, (name, splits))
             ref64 = oracle.sparse_mla_f64(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE,
                                           nthreads=oracle.default_threads())
@@ -323,7 +337,7 @@ def test_prefill_shaped_sampled(cuda, oracle, full_cache):
     qs = u16(q)[pick]
     ids = idx.cpu().numpy()[pick]
     want = oracle.sparse_mla(qs, rows, ids, W.SM_SCALE, n_splits=1, nthreads=oracle.default_threads(),
-                             groups=GROUPS, block_n=BLOCK, lazy=LAZY)
+                             groups=kernel_groups(idx.shape[-1], 1), block_n=BLOCK, lazy=LAZY)
     got = out[torch.as_tensor(pick, device=cuda)]
     compare(got, want, "prefill sample")
 
@@ -446,8 +460,9 @@ def test_merge_beyond_register_splits(cuda, oracle, small_cache):
         two = sparse_mla_merge(sparse_mla_partials(q, kv, idx, W.SM_SCALE, s), 2, 16, s)
         torch.cuda.synchronize()
         assert torch.equal(out, two), s
-        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s, groups=GROUPS,
-                                 block_n=BLOCK, lazy=LAZY, nthreads=oracle.default_threads())
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s,
+                                 groups=kernel_groups(idx.shape[-1], s), block_n=BLOCK, lazy=LAZY,
+                                 nthreads=oracle.default_threads())
         compare(out, want, ("merge loop path", s))
 
 
@@ -470,6 +485,51 @@ def test_gather_floor_diagnostic(cuda, small_cache):
         assert bool(torch.isfinite(buf.view(torch.float32)).all()) and out.shape == (8, 16, 512)
     with pytest.raises(RuntimeError):
         sparse_mla_gather_floor(q, kv, idx, 1)
+
+
+def test_three_key_group_splits(cuda, oracle, small_cache):
+    """Splits of exactly three 32-key tiles (65 to 96 indices) run on the
+    12-wave variant (three key-group streams, one round): against the oracle
+    with the same three streams and, within the bar, the reference's single
+    stream; a single split writing bf16 directly (96 indices), a padded head
+    group (20 heads), ragged last splits (224 in 3, 352 in 4, 2176 in 23 and
+    24 -- B=8's split policy), pads and indices outside the cache both ways;
+    all -1 gives exactly 0; the paged form of the same call is bit-identical
+    to the flat one."""
+    from titan_mla import triton_mla_sparse_attention, triton_mla_sparse_attention_paged
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    g = W.gen(cuda, 123)
+    for T, H, topk, splits in ((3, 16, 96, 1), (2, 20, 224, 3), (5, 16, 352, 4), (8, 16, 2176, 23),
+                               (4, 16, 2176, 24)):
+        assert kernel_groups(topk, splits) == 3
+        q = torch.randn(T, H, 512, generator=g, device=cuda).to(torch.bfloat16)
+        idx = torch.randint(-40, n + 40, (T, 1, topk), generator=g, device=cuda, dtype=torch.int32)
+        idx[0, :, topk // 2:] = -1
+        log_case("mla three key groups", T, H, topk, splits)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+        torch.cuda.synchronize()
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=3,
+                                 block_n=BLOCK, lazy=LAZY)
+        mx, mean = compare(out, want, ("three groups", T, H, topk, splits))
+        assert mean < 1e-4        # ~bf16 ulp-level agreement with its own reduction structure
+        single = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits, groups=1,
+                                   block_n=BLOCK)
+        compare(out, single, ("three groups vs single stream", T, H, topk, splits))
+        blank = triton_mla_sparse_attention(q, kv, torch.full_like(idx, -1), W.SM_SCALE, num_kv_splits=splits)
+        assert torch.equal(blank, torch.zeros_like(blank)), (T, H, topk, splits)
+    # paged: one request whose block table maps positions to the same rows
+    T, H, topk, splits, bs = 4, 16, 2176, 23, 64
+    q = torch.randn(T, H, 512, generator=g, device=cuda).to(torch.bfloat16)
+    idx = torch.randint(-8, n + 8, (T, 1, topk), generator=g, device=cuda, dtype=torch.int32)
+    flat = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+    pages = w["cache"].view(n // bs, bs, 528)
+    table = torch.arange(n // bs, device=cuda, dtype=torch.int32)[None, :]
+    req = torch.zeros(T, dtype=torch.int32, device=cuda)
+    paged = triton_mla_sparse_attention_paged(q, pages, idx, req, table, W.SM_SCALE, num_kv_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(paged, flat)
 
 
 def test_long_split_pair_kernel_edges(cuda, oracle, small_cache):
