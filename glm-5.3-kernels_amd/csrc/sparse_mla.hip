@@ -148,8 +148,8 @@ __device__ __forceinline__ void i8x16_to_bf16(const uint4 v, bf16x8& lo, bf16x8&
 
 // Shape of the split kernel for kG key groups of kSlices waves: two groups
 // take chunks of 8 tiles in 4 rounds (any decode split); three take one
-// round of 3 tiles (splits of at most 96 keys: B=8's 23 splits of 95 keys
-// in one round instead of two).
+// round of 3 tiles (splits of 65-96 keys: B=8's 23 splits of 95 keys in one
+// round instead of two); one takes a single tile (splits of at most 32).
 template <int kG>
 struct SplitShape {
   static constexpr int kWaves = kSlices * kG;
@@ -1179,21 +1179,23 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   // Long splits go to the pair kernel, whose masked keys read row 0 (page 0):
   // it needs a non-empty cache (seq_kv counts rows, or pages when paged).
   const bool pair = pipe && a.seq_kv > 0;
-  // Splits of exactly three tiles (65 to 96 keys) run in one round on three key groups.
+  // Splits of exactly three tiles (65 to 96 keys) run in one round on three
+  // key groups, splits of one tile on one key group.
   const bool three = a.split_len > 2 * kTile && a.split_len <= 3 * kTile;
-#define GLM53_THREE(M) hipLaunchKernelGGL((sparse_mla_kernel<M, false, 3>), grid, \
-                                          dim3(SplitShape<3>::kThreads), 0, st, a)
+  const bool one = a.split_len <= kTile;
+#define GLM53_KG(M, G) hipLaunchKernelGGL((sparse_mla_kernel<M, false, G>), grid, \
+                                          dim3(SplitShape<G>::kThreads), 0, st, a)
   if (mode == kPooledPos) {
     if (pair) GLM53_PAIR(kPooledPos); else if (pipe) GLM53_LAUNCH(kPooledPos, true);
-    else if (three) GLM53_THREE(kPooledPos); else GLM53_LAUNCH(kPooledPos, false);
+    else if (three) GLM53_KG(kPooledPos, 3); else if (one) GLM53_KG(kPooledPos, 1); else GLM53_LAUNCH(kPooledPos, false);
   } else if (mode == kPagedPos) {
     if (pair) GLM53_PAIR(kPagedPos); else if (pipe) GLM53_LAUNCH(kPagedPos, true);
-    else if (three) GLM53_THREE(kPagedPos); else GLM53_LAUNCH(kPagedPos, false);
+    else if (three) GLM53_KG(kPagedPos, 3); else if (one) GLM53_KG(kPagedPos, 1); else GLM53_LAUNCH(kPagedPos, false);
   } else {
     if (pair) GLM53_PAIR(kFlatRows); else if (pipe) GLM53_LAUNCH(kFlatRows, true);
-    else if (three) GLM53_THREE(kFlatRows); else GLM53_LAUNCH(kFlatRows, false);
+    else if (three) GLM53_KG(kFlatRows, 3); else if (one) GLM53_KG(kFlatRows, 1); else GLM53_LAUNCH(kFlatRows, false);
   }
-#undef GLM53_THREE
+#undef GLM53_KG
 #undef GLM53_PAIR
 #undef GLM53_LAUNCH
 }
@@ -1501,9 +1503,13 @@ extern "C" int glm53_sparse_mla_gather_floor(const void* q, int64_t sq_t, int64_
   const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
                   static_cast<unsigned>(a.heads_padded / kHeads));
   (void)hipGetLastError();
-  // the split kernel's workgroup shape for this split length (three key groups for 3-tile splits)
+  // the split kernel's workgroup shape for this split length (three key
+  // groups for 3-tile splits, one for 1-tile splits)
   if (a.split_len > 2 * kTile && a.split_len <= 3 * kTile)
     hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<3>, grid, dim3(SplitShape<3>::kThreads), 0,
+                       static_cast<hipStream_t>(stream), a);
+  else if (a.split_len <= kTile)
+    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<1>, grid, dim3(SplitShape<1>::kThreads), 0,
                        static_cast<hipStream_t>(stream), a);
   else
     hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<2>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);

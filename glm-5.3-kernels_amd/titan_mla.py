@@ -67,25 +67,28 @@ def _choose_num_kv_splits_mi355x(num_tokens: int, num_head_groups: int, index_to
                                  cu_count: int) -> int:
     """Split count used when the caller leaves num_kv_splits to the library.
 
-    The split kernel runs one 512-thread workgroup per (split, token, head
-    group) and needs ~106 KB of LDS, so one workgroup fits a compute unit.
-    Decode latency is set by the per-workgroup chain (index load -> row
-    gather -> tiles), so the split count is capped where every workgroup
-    still starts in the first wave (tokens * groups * splits <= CUs) and
-    each of the workgroup's two key groups gets a tile (two 32-key tiles per
-    split); under that cap it takes the fewest tiles per split, then the
-    fewest splits that give that many (fewer split partials for the merge).
-    B=1, 2, 4 at 2176 indices: 34 splits of 2 tiles; B=8: 23 splits of 3
-    (13.2 us per step over a 5-layer rotation against 13.4 us for the 17
-    splits of 4 tiles that a divisor of the tile count would give).  (The
-    reference's _choose_num_kv_splits targets Triton on 70 SMs and is kept
-    above, unchanged, for callers that want its exact answers.)
+    The split kernel runs one workgroup per (split, token, head group), one
+    key group of four waves per tile of a round, and one workgroup fits a
+    compute unit (up to ~136 KB of LDS).  Decode latency is set by the
+    per-workgroup chain (index load -> row gather -> tiles), so the split
+    count is capped where every workgroup still starts in the first wave
+    (tokens * groups * splits <= CUs) and, with more than one (token, head
+    group) unit, each split has two 32-key tiles (the merge reads every
+    split's partials, so more units call for fewer, longer splits); under
+    the cap it takes the fewest tiles per split, then the fewest splits that
+    give that many.  At 2176 indices: B=1 68 one-tile splits (9.35 us warm
+    against 10.1-10.5 us for 34 of two), B=2 and B=4 34 splits of 2 tiles
+    (B=2 at 68: 10.9 against 10.4 us), B=8 23 splits of 3 (13.1 us per step
+    over a 5-layer rotation against 13.4 us for 17 of 4).  (The reference's
+    _choose_num_kv_splits targets Triton on 70 SMs and is kept above,
+    unchanged, for callers that want its exact answers.)
     """
     base = num_tokens * num_head_groups
     if base == 0 or index_topk % _MIN_BLOCK_N:
         return 1
     tiles = index_topk // _MIN_BLOCK_N
-    cap = max(1, min(cu_count // base, tiles // 2))
+    min_tiles = 1 if base == 1 else 2
+    cap = max(1, min(cu_count // base, tiles // min_tiles))
     per_split = -(-tiles // cap)
     return -(-tiles // per_split)
 

@@ -105,22 +105,25 @@ def test_mla_and_writer_contract_assertions_on_cpu():
 
 def test_library_split_policy_table():
     """The library's auto split count (_choose_num_kv_splits_mi355x): capped
-    at tokens x head groups x splits <= CUs and two 32-key tiles per split,
-    the fewest tiles per split under the cap, then the fewest splits giving
-    that many.  Hand table at 256 CUs (and 70)."""
+    at tokens x head groups x splits <= CUs and, with more than one (token,
+    head group) unit, two 32-key tiles per split; the fewest tiles per split
+    under the cap, then the fewest splits giving that many.  Hand table at
+    256 CUs (and 70)."""
     from titan_mla import _choose_num_kv_splits_mi355x as pick
     table = {
-        (1, 1, 2176, 256): 34, (2, 1, 2176, 256): 34, (3, 1, 2176, 256): 34, (4, 1, 2176, 256): 34,
+        (1, 1, 2176, 256): 68,            # one unit: 68 one-tile splits
+        (2, 1, 2176, 256): 34, (3, 1, 2176, 256): 34, (4, 1, 2176, 256): 34,
+        (1, 2, 2176, 256): 34,            # two head groups: two units
         (8, 1, 2176, 256): 23,            # cap 32 -> 3 tiles per split -> ceil(68 / 3) = 23
         (16, 1, 2176, 256): 14,           # cap 16 -> 5 tiles per split -> 14
         (8, 4, 2176, 256): 8,             # 32 units: cap 8 -> 9 tiles per split -> 8
         (256, 1, 2176, 256): 1, (2048, 1, 2176, 256): 1, (300, 1, 2176, 256): 1,
         (1, 1, 32, 256): 1,               # one tile: nothing to split
-        (1, 1, 64, 256): 1,               # two tiles: one split keeps both key groups busy
-        (1, 1, 96, 256): 1, (1, 1, 128, 256): 2,
+        (1, 1, 64, 256): 2, (1, 1, 96, 256): 3, (1, 1, 128, 256): 4,
+        (2, 1, 64, 256): 1, (2, 1, 128, 256): 2,
         (1, 1, 2150, 256): 1,             # not a multiple of 32
         (1, 1, 16384, 256): 256,          # 512 tiles: 256 splits of 2 (the merge's loop path)
-        (1, 1, 2176, 70): 34,             # 34 <= 70
+        (1, 1, 2176, 70): 68,             # 68 <= 70
         (3, 1, 2176, 70): 23,             # cap 23 -> 3 tiles per split -> 23
         (0, 1, 2176, 256): 1,
     }

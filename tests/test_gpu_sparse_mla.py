@@ -40,10 +40,11 @@ def u16(t):
 
 def kernel_groups(topk, splits):
     """Online-softmax streams per split in the HIP kernel for this split
-    length: one (the pair kernel) past a chunk of 256 keys, three key groups
-    for splits of exactly three 32-key tiles, two otherwise."""
+    length: one past a chunk of 256 keys (the pair kernel) and for splits of
+    one 32-key tile (one key group), three key groups for splits of exactly
+    three tiles, two otherwise."""
     split_len = -(-topk // splits)
-    return 1 if split_len > 256 else 3 if 64 < split_len <= 96 else GROUPS
+    return 1 if split_len > 256 or split_len <= 32 else 3 if 64 < split_len <= 96 else GROUPS
 
 
 def rows_np(cache):
