@@ -52,6 +52,8 @@ def test_noalloc_equals_workspace_entry(cuda):
     stream = lib.stream_handle(cuda)
     cases = ((8, 16, 2176, 17, "B=8 x 17 splits: 2176 partial rows"),
              (2, 20, 1024, 8, "B=2, 20 heads x 8 splits: 512 partial rows (smaller, after the larger)"),
+             (8, 16, 2176, 23, "B=8 x 23 splits of three tiles (three key groups): 2944 partial rows"),
+             (1, 16, 2176, 68, "B=1 x 68 one-tile splits (one key group): 1088 partial rows"),
              (1, 16, 2176, 1, "single pass: no scratch"),
              (4, 64, 2048, 32, "exactly the limit: 4 x 32 x 64 = 8192 partial rows"))
     for T, H, topk, splits, tag in cases:
