@@ -604,14 +604,18 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
 //     registers).
 //   * The partial S^T buffer is single: a second barrier before a wave
 //     overwrites its half keeps it from racing the other wave's read.
-//   * Gathers run two tiles ahead and index loads four; no barrier waits
-//     for them (a workgroup barrier here waits only for LDS traffic).  Every
+//   * Gathers run one tile ahead and index loads three, and two waves share
+//     each SIMD (two workgroups of a CU's four): while one wave waits for its
+//     next tile's rows the other computes.  (Gathers two tiles ahead with one
+//     wave per SIMD needed 280 registers and ran 14 % slower.)  No barrier
+//     waits for the loads (a workgroup barrier here waits only for LDS
+//     traffic).  Every
 //     load is unconditional: a masked key reads row 0 (its score becomes
 //     -1e30, its weight and scale 0, and int8 codes are finite); a branch
 //     around the loads would make the compiler's wait before the next use
 //     count no load as outstanding, draining the prefetch every tile.
-//   * 38 KB of LDS per workgroup and up to 512 registers per wave (280
-//     used; at two waves per SIMD the kernel spills).
+//   * 38 KB of LDS per workgroup (four fit a CU's 160 KB) and at most 256
+//     registers per wave (249 used, no scratch).
 constexpr int kHalfLat = kLatent / 2;
 constexpr int kPairVStride = kHalfLat + 16;   // bf16 per LDS V row: 544 bytes
 constexpr int kPairRowBytes = kPairVStride * 2;
@@ -628,7 +632,7 @@ __device__ __forceinline__ int pair_vofs(int row, int col) {
 }
 
 template <int kMode>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void sparse_mla_pair_kernel(const MlaArgs a) {
   constexpr bool kPaged = kMode != kFlatRows;
   __shared__ PairShared sh;
@@ -684,11 +688,11 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
   // Key l of tile n is handled by lane l < 32 in three steps, each one tile
   // ahead of the next so that no step waits for a load younger than the
   // gathers in flight (loads complete in order):
-  //   load_raw (tile n - 4): its index (pooled mode: its pool id), read
+  //   load_raw (tile n - 3): its index (pooled mode: its pool id), read
   //     from an address clamped into the split, with no branch;
-  //   lookup   (tile n - 3): the position's block-table entry (paged modes;
+  //   lookup   (tile n - 2): the position's block-table entry (paged modes;
   //     flat rows need no load), again from a clamped address;
-  //   issue_rows (tile n - 2): the scale and the row gathers.
+  //   issue_rows (tile n - 1): the scale and the row gathers.
   // Positions past the split and invalid keys are masked in lookup and
   // issue_rows; masked keys read row 0 (unit 0 of the paged cache), which
   // exists because the launch requires a non-empty cache.  (Masking right
@@ -750,10 +754,11 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
     r.vmask = static_cast<uint32_t>(__ballot(lane < kTile && v >= 0));
   };
 
-  // One tile: convert + S^T + V to LDS, then the index of tile n + 4, the
-  // lookup of tile n + 3 and the gathers of tile n + 2, then the exchange,
-  // softmax and PV.  raw_s / look_s hold tile n + 2's index and lookup on
-  // entry (the slot of n's parity), raw_o / look_o tile n + 3's.
+  // One tile: convert + S^T + V to LDS, then the index of tile n + 3, the
+  // lookup of tile n + 2 and the gathers of tile n + 1 (into the registers
+  // this tile's rows just left), then the exchange, softmax and PV.  On
+  // entry raw_s holds tile n + 2's index (the slot of n's parity) and look_o
+  // tile n + 1's lookup.
   auto tile = [&](int n, Rows& cur, int& raw_s, int& raw_o, Look& look_s, Look& look_o) {
     f32x4 s_part[2];
 #pragma unroll
@@ -785,13 +790,13 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
         const float v = __shfl(cur.sv, 16 * u + 4 * g + r, 64);
         sc[4 * u + r] = (kv_ok >> (4 * u + r)) & 1 ? v : 0.f;
       }
-    // the registers of this tile are free: gathers of tile n + 2, index of tile n + 4
+    // the registers of this tile are free: gathers of tile n + 1, index of tile n + 3
     // (kept below the conversions: hoisted above them the loads would hold a
     // second tile's registers while the converted operands are still live)
     __builtin_amdgcn_sched_barrier(0);
-    raw_s = load_raw(n + 4);
-    look_o = lookup(raw_o, n + 3);
-    issue_rows(cur, look_s);
+    raw_o = load_raw(n + 3);
+    look_s = lookup(raw_s, n + 2);
+    issue_rows(cur, look_o);
     __syncthreads();
 
     // Full scores: wave 0's partial + wave 1's, the same order in both waves.
@@ -850,20 +855,19 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
 
   // Tiles go in pairs (an odd count ends with a fully masked tile, which
   // changes nothing): no branch in the loop body.
-  Rows ra, rb;
+  Rows ra;                               // the one tile of rows in flight
   int r0 = -1, r1 = -1;                  // raw slots (even, odd tiles)
   Look l0 = {-1, -1}, l1 = {-1, -1};     // lookup slots
   if (ntiles > 0) {
-    const int i0 = load_raw(0), i1 = load_raw(1), i2 = load_raw(2);
-    r1 = load_raw(3);
-    const Look k0 = lookup(i0, 0), k1 = lookup(i1, 1);
-    l0 = lookup(i2, 2);
+    const int i0 = load_raw(0), i1 = load_raw(1);
+    r0 = load_raw(2);
+    const Look k0 = lookup(i0, 0);
+    l1 = lookup(i1, 1);
     issue_rows(ra, k0);
-    issue_rows(rb, k1);
   }
   for (int n = 0; n < ntiles; n += 2) {
     tile(n, ra, r0, r1, l0, l1);
-    tile(n + 1, rb, r1, r0, l1, l0);
+    tile(n + 1, ra, r1, r0, l1, l0);
   }
 
   // Both waves hold the same m and l; each writes its latent half.
