@@ -241,7 +241,7 @@ def test_random_shapes(cuda, oracle, small_cache):
     kv = w["cache"].view(n, 1, 528)
     rng = np.random.default_rng(4242)
     g = W.gen(cuda, 4242)
-    for case in range(16):
+    for case in range(40):
         T = int(rng.integers(1, 7))
         heads = int(rng.choice([1, 4, 8, 16, 20, 32]))
         topk = 32 * int(rng.integers(1, 81))
@@ -486,6 +486,32 @@ def test_gather_floor_diagnostic(cuda, small_cache):
         assert bool(torch.isfinite(buf.view(torch.float32)).all()) and out.shape == (8, 16, 512)
     with pytest.raises(RuntimeError):
         sparse_mla_gather_floor(q, kv, idx, 1)
+
+
+def test_split_length_boundaries(cuda, oracle, small_cache):
+    """Split lengths at every boundary between the kernel variants, 2176
+    indices with pads and out-of-range values: 32 keys (one key group), 33
+    and 64 (two groups, one round), 66 and 95 (three groups), 99 and 242 (two
+    groups, two to eight tiles), 272 (the pair kernel) -- each against the
+    oracle with the same stream structure."""
+    from titan_mla import triton_mla_sparse_attention
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    g = W.gen(cuda, 321)
+    T, H, topk = 2, 16, 2176
+    q = torch.randn(T, H, 512, generator=g, device=cuda).to(torch.bfloat16)
+    idx = torch.randint(-40, n + 40, (T, 1, topk), generator=g, device=cuda, dtype=torch.int32)
+    idx[1, :, 1900:] = -1
+    for splits, split_len in ((68, 32), (66, 33), (34, 64), (33, 66), (23, 95), (22, 99), (9, 242), (8, 272)):
+        assert -(-topk // splits) == split_len
+        log_case("mla split-length boundary", splits, split_len)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+        torch.cuda.synchronize()
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits,
+                                 groups=kernel_groups(topk, splits), block_n=BLOCK, lazy=LAZY)
+        mx, mean = compare(out, want, ("split length", splits, split_len))
+        assert mean < 1e-4
 
 
 def test_three_key_group_splits(cuda, oracle, small_cache):
