@@ -887,8 +887,12 @@ namespace {
 // How the top-k of rows of max_len columns runs: one final workgroup over
 // the row (direct, P keys per thread), or the chunk stage (chunks of
 // 512 * chunk_p positions, chunk_len > k) then the final stage over
-// chunks * k candidates, or the sweep kernel.  Among chunk sizes the one with
-// the fewest keys per thread over the two stages wins.
+// chunks * k candidates, or the sweep kernel.  For a few rows (latency) the
+// chunk size with the fewest keys per thread over the two stages wins; from
+// 32 rows on (throughput: the chunk stage alone is many workgroups per CU)
+// 8192-position chunks, half the workgroups and candidates (2048 rows x
+// 65536 positions, k = 512: 283 -> 242 us; 32 rows 16.6 -> 15.6 us; 16 rows
+// 15.0 -> 15.5 us, so the latency choice stays below 32).
 struct TopkPlan {
   enum Mode { kDirect, kChunked, kSweepMode } mode;
   int chunk_p, final_p, chunks, chunk_len;
@@ -900,7 +904,9 @@ int final_p_for(int64_t n) {
   return 0;
 }
 
-TopkPlan plan_topk(int64_t max_len, int64_t k) {
+constexpr int64_t kTopkThroughputRows = 32;
+
+TopkPlan plan_topk(int64_t num_rows, int64_t max_len, int64_t k) {
   if (max_len <= int64_t(kFinalThreads) * 4) return {TopkPlan::kDirect, 0, 4, 0, 0};
   TopkPlan best{TopkPlan::kSweepMode, 0, 0, 0, 0};
   int best_cost = 1 << 30;
@@ -911,8 +917,9 @@ TopkPlan plan_topk(int64_t max_len, int64_t k) {
     if (chunks < 2) continue;
     const int fp = final_p_for(chunks * k);
     if (fp == 0) continue;
-    if (p + fp < best_cost) {
-      best_cost = p + fp;
+    const int cost = num_rows >= kTopkThroughputRows && p == 16 ? 0 : p + fp;
+    if (cost < best_cost) {
+      best_cost = cost;
       best = {TopkPlan::kChunked, p, fp, static_cast<int>(chunks), static_cast<int>(len_c)};
     }
   }
@@ -942,7 +949,7 @@ void launch_final(bool cand, dim3 grid, hipStream_t st, const TopkArgs& a) {
 
 extern "C" int64_t glm53_indexer_topk_workspace_bytes(int64_t num_rows, int64_t max_len, int64_t k) {
   if (!topk_shape_ok(num_rows, max_len, k)) return 0;
-  return topk_ws_bytes(plan_topk(max_len, k), num_rows, k);
+  return topk_ws_bytes(plan_topk(num_rows, max_len, k), num_rows, k);
 }
 
 extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t* lengths, int64_t num_rows,
@@ -952,7 +959,7 @@ extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t
   if (!topk_shape_ok(num_rows, max_len, k) || sl < max_len || so < k) return GLM53_ERR_BAD_SHAPE;
   if (num_rows == 0) return 0;
   if (!aligned(logits, 4)) return GLM53_ERR_MISALIGNED;
-  const TopkPlan plan = plan_topk(max_len, k);
+  const TopkPlan plan = plan_topk(num_rows, max_len, k);
   const int64_t need = topk_ws_bytes(plan, num_rows, k);
   if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 16))) return GLM53_ERR_WORKSPACE;
   TopkArgs a{logits, sl, lengths, static_cast<int>(max_len), static_cast<int>(k), out, so, nullptr, nullptr,

@@ -148,20 +148,23 @@ def test_topk_ties_specials_and_short_rows(cuda, oracle):
         assert np.array_equal(got.cpu().numpy(), want), k
 
 
+@pytest.mark.parametrize("copies", [1, 4])
 @pytest.mark.parametrize("n,k", [
     (4096, 512),      # one workgroup over the row, 4 keys per thread
     (32768, 16384),   # one workgroup over the row, 32 keys per thread (chunks would not exceed k)
-    (65536, 512),     # chunks of 4096, 8192 candidates
+    (65536, 512),     # chunks of 4096, 8192 candidates (from 32 rows: chunks of 8192, 4096)
     (20000, 8192),    # chunks of 16384, 16384 candidates
     (140000, 4096),   # too many candidates: sweeps over the row
 ])
-def test_topk_every_plan(cuda, oracle, n, k):
+def test_topk_every_plan(cuda, oracle, n, k, copies):
     """Each execution plan of the top-k, with ragged, clamped, tied and NaN
-    rows; chunk boundaries at 4096, 8192 and 16384 positions."""
+    rows; chunk boundaries at 4096, 8192 and 16384 positions.  copies = 4
+    repeats the row set (40 rows), which takes the throughput plan (8192-
+    position chunks) where it applies."""
     import torch
     from sparse_indexer import indexer_topk
-    g = torch.Generator(device=cuda).manual_seed(n + k)
-    lens_list = [n, n - 1, min(n, 4097), min(n, 8193), min(n, 16385), k + 1, k, 3, -5, n + 1000]
+    g = torch.Generator(device=cuda).manual_seed(n + k + copies)
+    lens_list = [n, n - 1, min(n, 4097), min(n, 8193), min(n, 16385), k + 1, k, 3, -5, n + 1000] * copies
     rows = len(lens_list)
     x = torch.randn(rows, n, generator=g, device=cuda)
     x[1] = torch.randint(0, 3, (n,), generator=g, device=cuda).float()     # heavy ties
