@@ -642,6 +642,20 @@ def main():
                                   "gbs_rotation": round(bytes_p / (us_pr * 1e-6) / 1e9, 1),
                                   "hbm_frac_rotation": round(bytes_p / (us_pr * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
                                   "tflops_warm": round(flops_p / (us_p * 1e-6) / 1e12, 2)}
+        # The same call in request-relative form (a vLLM-style paged prefill):
+        # one request whose 262144 tokens sit in 4096 pages of 64 rows at
+        # random places, the indices positions within the request; the block
+        # table lookup runs inside the attention's gather.
+        from titan_mla import triton_mla_sparse_attention_paged
+        pp_pages = cache8.view(n_rows // 64, 64, W.ROW_BYTES)
+        pp_bt = torch.randperm(pp_pages.shape[0], generator=g8, device=dev).to(torch.int32)[None, :].contiguous()
+        pp_req = torch.zeros(qp.shape[0], dtype=torch.int32, device=dev)
+        ppg, _ = capture(torch, lambda: triton_mla_sparse_attention_paged(qp, pp_pages, idxp, pp_req, pp_bt,
+                                                                           W.SM_SCALE), 3)
+        ppg.replay()
+        us_pp = timer.median_loop(ppg, 3) / 3
+        del ppg
+        extra["prefill_t2048"]["us_per_call_paged_warm"] = round(us_pp, 1)
         # the prefill-shaped call's write: 2048 rows into randperm slots,
         # `unroll` calls per graph (one call per graph would time the graph
         # launch, ~15 us, not the kernel's ~3 us)
