@@ -512,6 +512,18 @@ def test_split_length_boundaries(cuda, oracle, small_cache):
                                  groups=kernel_groups(topk, splits), block_n=BLOCK, lazy=LAZY)
         mx, mean = compare(out, want, ("split length", splits, split_len))
         assert mean < 1e-4
+    # single splits written as bf16 directly: one tile (one key group), three
+    # tiles (three key groups), and 20 heads (a padded head group)
+    for topk, heads in ((32, 16), (96, 16), (32, 20), (96, 20)):
+        q = torch.randn(3, heads, 512, generator=g, device=cuda).to(torch.bfloat16)
+        idx = torch.randint(-8, n + 8, (3, 1, topk), generator=g, device=cuda, dtype=torch.int32)
+        log_case("mla single split", topk, heads)
+        out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=1)
+        torch.cuda.synchronize()
+        want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=1,
+                                 groups=kernel_groups(topk, 1), block_n=BLOCK, lazy=LAZY)
+        mx, mean = compare(out, want, ("single split", topk, heads))
+        assert mean < 1e-4
 
 
 def test_three_key_group_splits(cuda, oracle, small_cache):
