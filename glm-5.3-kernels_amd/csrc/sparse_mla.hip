@@ -502,6 +502,27 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
     }
   }
 
+  // ---- one key group: nothing to merge.  Each wave stores its 16 heads x
+  // 128 latents straight from the MFMA C layout (16 heads x 64-byte pieces
+  // per store instruction), with no LDS round trip and no barrier.
+  if constexpr (kG == 1) {
+    const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
+    if (!head_ok) return;
+    const bool direct = a.num_splits == 1 && !a.partials_only;
+    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) {
+      const float4 v = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l, acc[dt][2] * inv_l, acc[dt][3] * inv_l);
+      const int col = kSlice * sl + 16 * dt + 4 * g;   // head c, latents 128 sl + 16 dt + 4 g + [0, 4)
+      if (direct)
+        *reinterpret_cast<uint2*>(a.out + t * a.so_t + head * a.so_h + col) =
+            make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+      else
+        *reinterpret_cast<float4*>(a.part + row * kLatent + col) = v;
+    }
+    if (!direct && sl == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
+    return;
+  } else {
   // ---- combine the key groups and write the 16 result rows.  The MFMA
   // C layout scatters a lane's values over 16 rows (16 x 64-byte pieces per
   // store instruction, which the memory pipeline issues ~2.5x slower than
@@ -579,6 +600,7 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
       *reinterpret_cast<float4*>(pp + 256 + 4 * lane) = fin4(256 + 4 * lane);
       if (lane == 0) a.lse[row] = (mm + log2f(l)) * kLn2;
     }
+  }
   }
 }
 
