@@ -967,8 +967,17 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
         fold ^= *reinterpret_cast<const uint32_t*>(a.kv + static_cast<int64_t>(v) * a.skv + kLatent);
     }
   }
-  // a finite float from the folded bits, stored where the split kernel stores
+  // a finite float from the folded bits, stored where and as the split kernel stores
   const float x = static_cast<float>(fold & 0xffff);
+  if constexpr (kG == 1) {   // straight from the C layout: head c, latents 128 sl + 16 dt + 4 g + [0, 4)
+    if (head >= a.num_heads) return;
+    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+      *reinterpret_cast<float4*>(a.part + row * kLatent + kSlice * sl + 16 * dt + 4 * g) = make_float4(x, x, x, x);
+    if (sl == 0 && g == 0) a.lse[row] = x;
+    return;
+  }
   constexpr int kRowsPerWave = (kHeads + kWaves - 1) / kWaves;
 #pragma unroll
   for (int k = 0; k < kRowsPerWave; k++) {

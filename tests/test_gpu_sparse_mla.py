@@ -468,9 +468,9 @@ def test_merge_beyond_register_splits(cuda, oracle, small_cache):
 
 
 def test_gather_floor_diagnostic(cuda, small_cache):
-    """The memory-chain probe runs on the decode grids, fills the partials
-    buffer the merge reads (junk, finite), and refuses splits longer than one
-    chunk of gathers."""
+    """The memory-chain probe runs on the decode grids of every split-kernel
+    shape, fills the whole partials buffer the merge reads (junk, finite),
+    and refuses splits longer than one chunk of gathers."""
     from titan_mla import sparse_mla_gather_floor, sparse_mla_merge
     w, _ = small_cache
     n = w["n_rows"]
@@ -478,7 +478,7 @@ def test_gather_floor_diagnostic(cuda, small_cache):
     g = W.gen(cuda, 21)
     q = torch.randn(8, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
     idx = torch.randint(-8, n, (8, 1, 2176), generator=g, device=cuda, dtype=torch.int32)
-    for s in (17, 34):
+    for s in (17, 34, 23, 68):   # two key groups, three (95-key splits), one (32-key splits)
         log_case("gather floor", s)
         buf = sparse_mla_gather_floor(q, kv, idx, s)
         out = sparse_mla_merge(buf, 8, 16, s)
