@@ -55,7 +55,7 @@ constexpr int kChunkTiles = 8;         // tiles whose gathers are in flight toge
 constexpr int kRounds = kChunkTiles / kGroups;
 constexpr int kMergeLanes = 8;         // split lanes per output chunk in the LSE merge
 constexpr int kMaxMergeSplits = 1024;
-constexpr int kRowStride = kLatent + 4;  // fp32 per LDS result row: 16 rows hit 64 distinct banks
+constexpr int kParkStride = kSlice + 4;  // fp32 per parked row (16 heads x 128 latents per wave): rows 4 banks apart
 constexpr float kNegLarge = -1.0e30f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -162,13 +162,8 @@ struct SplitShape {
 template <int kG>
 struct __attribute__((aligned(16))) MlaShared {
   using S = SplitShape<kG>;
-  union {
-    uint16_t vbuf[S::kWaves][kTile][kVStride];       // per-wave bf16 V slice of a tile
-    struct {
-      float rows[kG][kHeads][kRowStride];              // each key group's acc, row-major
-      float ml[kG][kHeads][2];                         // each key group's (m, l) per head
-    } fin;
-  };
+  uint16_t vbuf[S::kWaves][kTile][kVStride];         // per-wave bf16 V slice of a tile, then its parked acc
+  float ml[kG][kHeads][2];                             // each key group's (m, l) per head
   float4 red[S::kRedBufs][kG][kSlices][2][64];         // partial S^T per slice: [half][lane]
   float scl[2][S::kChunkTiles][kTile];                 // row scales of the chunk
 };
@@ -236,6 +231,14 @@ __device__ __forceinline__ int pooled_position(PoolAt pool, int num_pools, int p
 // banks; the 16-byte chunks of rows 8-15 of every 16 (row bit 3) are XOR-
 // swapped in pairs so that a 16-byte write of 16 consecutive rows at one
 // column is conflict-free too (without it rows r and r + 8 share banks).
+// Wave w's parked accumulators: its V buffer viewed as 16 rows of
+// kParkStride floats (8448 bytes of the buffer's 9216).
+template <class Shared>
+__device__ __forceinline__ float* park_of(Shared& sh, int w) {
+  static_assert(kHeads * kParkStride * 4 <= kTile * kVStride * 2, "a wave's park fits its V buffer");
+  return reinterpret_cast<float*>(&sh.vbuf[w][0][0]);
+}
+
 template <class Shared>
 __device__ __forceinline__ uint16_t* vbuf_at(Shared& sh, int w, int row, int col) {
   const int chunk = (col >> 3) ^ ((row >> 3) & 1);
@@ -526,18 +529,18 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
   // ---- combine the key groups and write the 16 result rows.  The MFMA
   // C layout scatters a lane's values over 16 rows (16 x 64-byte pieces per
   // store instruction, which the memory pipeline issues ~2.5x slower than
-  // contiguous ones), so both key groups park their accumulators row-major
-  // in LDS and every wave then finishes two whole rows with contiguous
-  // 1 KB stores.
-  __syncthreads();  // vbuf is free
+  // contiguous ones), so every wave parks its 16 heads x 128 latents
+  // row-major in its own V buffer (which no other wave reads, so parking
+  // waits for nobody), and after one barrier every wave finishes whole rows
+  // with contiguous 1 KB stores.
   {
-    float* rp = &sh.fin.rows[kg][c][kSlice * sl + 4 * g];
+    float* rp = park_of(sh, w) + c * kParkStride + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
       *reinterpret_cast<float4*>(rp + 16 * dt) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
     if (sl == 0 && g == 0) {
-      sh.fin.ml[kg][c][0] = m_run;
-      sh.fin.ml[kg][c][1] = l_run;
+      sh.ml[kg][c][0] = m_run;
+      sh.ml[kg][c][1] = l_run;
     }
   }
   __syncthreads();
@@ -553,26 +556,31 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
     float mm = kNegLarge;
 #pragma unroll
     for (int i = 0; i < kG; i++) {
-      mg[i] = sh.fin.ml[i][r][0];
+      mg[i] = sh.ml[i][r][0];
       mm = i == 0 ? mg[0] : fmaxf(mm, mg[i]);
     }
     float l = 0.f;
 #pragma unroll
     for (int i = 0; i < kG; i++) {
       ag[i] = fast_exp2(mg[i] - mm);
-      const float li = sh.fin.ml[i][r][1] * ag[i];
+      const float li = sh.ml[i][r][1] * ag[i];
       l = i == 0 ? li : l + li;
     }
     // 1 / l once, then multiplies (the reference divides; the two differ by
     // at most one fp32 ulp before the bf16 / fp32 store).
     const float inv_l = 1.f / (l > 0.f ? l : 1.f);
     // key groups added in order: (x0 a0 + x1 a1) + x2 a2
+    // latent col of head r for key group i: in the park of wave (i, col / 128)
+    auto parked = [&](int i, int col) {
+      return *reinterpret_cast<const float4*>(park_of(sh, i * kSlices + col / kSlice) + r * kParkStride +
+                                              col % kSlice);
+    };
     auto fin4 = [&](int col) {
-      float4 v = *reinterpret_cast<const float4*>(&sh.fin.rows[0][r][col]);
+      float4 v = parked(0, col);
       v = make_float4(v.x * ag[0], v.y * ag[0], v.z * ag[0], v.w * ag[0]);
 #pragma unroll
       for (int i = 1; i < kG; i++) {
-        const float4 x = *reinterpret_cast<const float4*>(&sh.fin.rows[i][r][col]);
+        const float4 x = parked(i, col);
         v = make_float4(v.x + x.x * ag[i], v.y + x.y * ag[i], v.z + x.z * ag[i], v.w + x.w * ag[i]);
       }
       return make_float4(v.x * inv_l, v.y * inv_l, v.z * inv_l, v.w * inv_l);
