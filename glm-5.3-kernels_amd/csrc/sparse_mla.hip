@@ -288,24 +288,6 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
   const int32_t* pools_t = kMode == kPooledPos ? a.pools + t * a.sp_t : nullptr;
   const int seq_len_t = kMode == kPooledPos && a.seq_lens ? a.seq_lens[t] : -1;
 
-  // Q^T fragment (B operand of S^T = K Q^T): head c, latents 128 sl + 16g +
-  // [0, 16) and 128 sl + 64 + 16g + [0, 16) -> four K-steps of 8 (the same
-  // latents as the lane's gathered key bytes).
-  bf16x8 qf[4];
-  {
-    uint4 z = make_uint4(0, 0, 0, 0);
-    uint4 q0 = z, q1 = z, q2 = z, q3 = z;
-    if (head_ok) {
-      const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + head * a.sq_h +
-                                                       kSlice * sl + 16 * g);
-      q0 = qp[0]; q1 = qp[1]; q2 = qp[8]; q3 = qp[9];
-    }
-    qf[0] = __builtin_bit_cast(bf16x8, q0);
-    qf[1] = __builtin_bit_cast(bf16x8, q1);
-    qf[2] = __builtin_bit_cast(bf16x8, q2);
-    qf[3] = __builtin_bit_cast(bf16x8, q3);
-  }
-
   f32x4 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -344,6 +326,12 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
         v = to_page_unit(bt_req, max_blocks, a.block_size, a.num_blocks, a.page_units, a.row_units, v);
       else if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv)
         v = -1;
+      // The row scale first: issued after the rows, its load waited for them
+      // (its register reused one of theirs), a second round trip per split.
+      sv[r] = 0.f;
+      if (sl == 0 && lane < kTile && v >= 0)
+        sv[r] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(v) * (kPaged ? 16 : a.skv) +
+                                                kLatent);
 #pragma unroll
       for (int u = 0; u < 2; u++) {
         const int kid = __shfl(v, 16 * u + c, 64);
@@ -356,10 +344,6 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
           kd[r][u][1] = rp[4];   // slice bytes 64 + 16g + [0, 16): its last 64
         }
       }
-      sv[r] = 0.f;
-      if (sl == 0 && lane < kTile && v >= 0)
-        sv[r] = *reinterpret_cast<const float*>(a.kv + static_cast<int64_t>(v) * (kPaged ? 16 : a.skv) +
-                                                kLatent);
       vmask[r] = static_cast<uint32_t>(__ballot(v >= 0));
     }
   };
@@ -373,12 +357,33 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
     load_ids(start, idc);
     issue_rows(start, idc, kdc, svc, vmc);
   }
-  for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile, cbuf ^= 1) {
+  // A one-chunk (decode) split requests its indices before q: they head the
+  // dependent index -> row chain, while q is first needed by the products.
+  // Its chunk runs outside any loop, so no loop-carried wait makes the index
+  // load wait for q.
+  if (!kPipe && start < end) load_ids(start, idc);
+
+  // Q^T fragment (B operand of S^T = K Q^T): head c, latents 128 sl + 16g +
+  // [0, 16) and 128 sl + 64 + 16g + [0, 16) -> four K-steps of 8 (the same
+  // latents as the lane's gathered key bytes).
+  // The loads are unconditional (a padded head reads head 0 and is zeroed
+  // after): under a branch the compiler's wait for the index load would also
+  // wait for them.
+  bf16x8 qf[4];
+  {
+    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (head_ok ? head : 0) * a.sq_h +
+                                                     kSlice * sl + 16 * g);
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    const uint4 q0 = qp[0], q1 = qp[1], q2 = qp[8], q3 = qp[9];
+    qf[0] = __builtin_bit_cast(bf16x8, head_ok ? q0 : z);
+    qf[1] = __builtin_bit_cast(bf16x8, head_ok ? q1 : z);
+    qf[2] = __builtin_bit_cast(bf16x8, head_ok ? q2 : z);
+    qf[3] = __builtin_bit_cast(bf16x8, head_ok ? q3 : z);
+  }
+  if (!kPipe && start < end) issue_rows(start, idc, kdc, svc, vmc);
+
+  auto consume_chunk = [&](const int c0) {
     const int c1 = c0 + kChunkTiles * kTile;
-    if (!kPipe) {
-      load_ids(c0, idc);
-      issue_rows(c0, idc, kdc, svc, vmc);
-    }
     if (sl == 0 && lane < kTile) {
 #pragma unroll
       for (int r = 0; r < kRounds; r++) sh.scl[cbuf][kG * r + kg][lane] = svc[r];
@@ -492,17 +497,23 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
       }
       acc_zero = false;
     }
-    if (!kPipe) continue;
+  };
+  if constexpr (kPipe) {
+    for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile, cbuf ^= 1) {
+      consume_chunk(c0);
 #pragma unroll
-    for (int r = 0; r < kRounds; r++) {
-      vmc[r] = vmn[r];
-      svc[r] = svn[r];
+      for (int r = 0; r < kRounds; r++) {
+        vmc[r] = vmn[r];
+        svc[r] = svn[r];
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
-        kdc[r][u][0] = kdn[r][u][0];
-        kdc[r][u][1] = kdn[r][u][1];
+        for (int u = 0; u < 2; u++) {
+          kdc[r][u][0] = kdn[r][u][0];
+          kdc[r][u][1] = kdn[r][u][1];
+        }
       }
     }
+  } else if (start < end) {
+    consume_chunk(start);   // split_len <= kChunkTiles * kTile: one chunk
   }
 
   // ---- one key group: nothing to merge.  Each wave stores its 16 heads x
@@ -930,7 +941,6 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
 template <int kG>
 __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_floor_kernel(const MlaArgs a) {
   constexpr int kWaves = SplitShape<kG>::kWaves;
-  constexpr int kChunkTiles = SplitShape<kG>::kChunkTiles;
   constexpr int kRounds = SplitShape<kG>::kRounds;
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
   if ((gridDim.y * gridDim.z) % 8 == 0) {
@@ -950,30 +960,49 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
   const int end = min(start + a.split_len, a.topk);
   const int32_t* idx_t = a.idx + t * a.si_t;
   const int head = hg * kHeads + c;
-  uint32_t fold = 0;
-  if (head < a.num_heads) {
-    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + head * a.sq_h + kSlice * sl + 16 * g);
-    const uint4 q0 = qp[0], q1 = qp[1], q2 = qp[8], q3 = qp[9];
-    fold = q0.x ^ q1.y ^ q2.z ^ q3.w;
+  // The split kernel's load order: the split's indices, q, then per tile the
+  // row scale and the rows, all in flight before any is used (decode splits
+  // are one chunk: split_len <= kChunkTiles * kTile, checked by the host).
+  int ids[kRounds];
+#pragma unroll
+  for (int r = 0; r < kRounds; r++) {
+    const int pos = start + (kG * r + kg) * kTile + (lane & 31);
+    ids[r] = pos < end ? idx_t[pos] : -1;
   }
-  for (int c0 = start; c0 < end; c0 += kChunkTiles * kTile) {
+  const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (head < a.num_heads ? head : 0) * a.sq_h +
+                                                   kSlice * sl + 16 * g);
+  const uint4 q0 = qp[0], q1 = qp[1], q2 = qp[8], q3 = qp[9];
+  uint32_t sv[kRounds];
+  uint4 kd[kRounds][2][2];
 #pragma unroll
-    for (int r = 0; r < kRounds; r++) {
-      const int pos = c0 + (kG * r + kg) * kTile + (lane & 31);
-      int v = pos < end ? idx_t[pos] : -1;
-      if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv) v = -1;
+  for (int r = 0; r < kRounds; r++) {
+    int v = ids[r];
+    if (v < 0 || static_cast<int64_t>(v) >= a.seq_kv) v = -1;
+    sv[r] = 0;
+    if (sl == 0 && lane < kTile && v >= 0)
+      sv[r] = *reinterpret_cast<const uint32_t*>(a.kv + static_cast<int64_t>(v) * a.skv + kLatent);
+    // Row loads unconditional (a masked key reads row 0, then counts 0; the
+    // host requires a non-empty cache): a branch around them made the
+    // compiler copy the first load's result before issuing the second.
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int kid = __shfl(v, 16 * u + c, 64);
-        if (kid >= 0) {
-          const uint4* rp = reinterpret_cast<const uint4*>(a.kv + static_cast<int64_t>(kid) * a.skv + kSlice * sl + 16 * g);
-          const uint4 k0 = rp[0], k1 = rp[4];
-          fold ^= k0.x ^ k0.y ^ k0.z ^ k0.w ^ k1.x ^ k1.y ^ k1.z ^ k1.w;
-        }
-      }
-      if (sl == 0 && lane < kTile && v >= 0)
-        fold ^= *reinterpret_cast<const uint32_t*>(a.kv + static_cast<int64_t>(v) * a.skv + kLatent);
+    for (int u = 0; u < 2; u++) {
+      const int kid = __shfl(v, 16 * u + c, 64);
+      const uint4* rp = reinterpret_cast<const uint4*>(a.kv + static_cast<int64_t>(max(kid, 0)) * a.skv +
+                                                       kSlice * sl + 16 * g);
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      const uint4 k0 = rp[0], k1 = rp[4];
+      kd[r][u][0] = kid >= 0 ? k0 : z;
+      kd[r][u][1] = kid >= 0 ? k1 : z;
     }
+  }
+  uint32_t fold = head < a.num_heads ? q0.x ^ q1.y ^ q2.z ^ q3.w : 0u;   // folded last: no early wait
+#pragma unroll
+  for (int r = 0; r < kRounds; r++) {
+    fold ^= sv[r];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+      fold ^= kd[r][u][0].x ^ kd[r][u][0].y ^ kd[r][u][0].z ^ kd[r][u][0].w ^
+              kd[r][u][1].x ^ kd[r][u][1].y ^ kd[r][u][1].z ^ kd[r][u][1].w;
   }
   // a finite float from the folded bits, stored where and as the split kernel stores
   const float x = static_cast<float>(fold & 0xffff);
@@ -1540,6 +1569,7 @@ extern "C" int glm53_sparse_mla_gather_floor(const void* q, int64_t sq_t, int64_
   if (!partials || partials_bytes < need) return GLM53_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(partials) % 16) return GLM53_ERR_MISALIGNED;
   if (a.split_len > kChunkTiles * kTile) return GLM53_ERR_BAD_SHAPE;   // decode splits only
+  if (seq_kv < 1) return GLM53_ERR_BAD_SHAPE;                          // masked keys read row 0
   const int64_t rows = partial_rows(num_tokens, num_heads, num_splits);
   a.part = static_cast<float*>(partials);
   a.lse = static_cast<float*>(partials) + rows * kLatent;

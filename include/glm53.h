@@ -219,9 +219,11 @@ int glm53_sparse_mla_partials(const void* q, int64_t sq_t, int64_t sq_h,
  * Diagnostic, no counterpart in the reference: the memory chain of
  * glm53_sparse_mla_partials alone for decode splits (at most 256 indices per
  * split) -- the same grid, index loads, row gathers, scale loads and
- * partial/LSE stores, with no arithmetic (the partials hold junk).  Its time
- * is the floor that the split kernel's conversions, products and softmax
- * add to; bench.py reports both.
+ * partial/LSE stores, issued in the split kernel's order and all in flight
+ * before any is used, with no arithmetic (the partials hold junk).  Its
+ * time is the floor that the split kernel's conversions, products and
+ * softmax add to; bench.py reports both.  Needs seq_kv >= 1 (masked keys
+ * read row 0).
  */
 int glm53_sparse_mla_gather_floor(const void* q, int64_t sq_t, int64_t sq_h,
                                   const void* kv, int64_t skv_t, int64_t seq_kv,

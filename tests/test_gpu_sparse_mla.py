@@ -486,6 +486,8 @@ def test_gather_floor_diagnostic(cuda, small_cache):
         assert bool(torch.isfinite(buf.view(torch.float32)).all()) and out.shape == (8, 16, 512)
     with pytest.raises(RuntimeError):
         sparse_mla_gather_floor(q, kv, idx, 1)
+    with pytest.raises(RuntimeError):   # masked keys read row 0: an empty cache is refused
+        sparse_mla_gather_floor(q, kv[:0], idx, 68)
 
 
 def test_split_length_boundaries(cuda, oracle, small_cache):
