@@ -82,20 +82,29 @@ __global__ __launch_bounds__(256) void store_int8_vec(const uint16_t* __restrict
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave) * ROWS;
+  // The rows' latents are requested before their slots and without waiting
+  // for them (a row past n re-reads row n - 1, a skipped row is read and
+  // dropped): behind each slot's scalar load the wave paid a memory round
+  // trip per row before its latents were even requested.
   uint4 v[ROWS];
   int64_t slot[ROWS];
 #pragma unroll
   for (int r = 0; r < ROWS; r++) {
-    const int64_t row = row0 + r;
-    slot[r] = row < n ? load_slot(slots, slots_i64, row) : -1;
-    if (slot[r] >= capacity) slot[r] = -1;
-    v[r] = make_uint4(0, 0, 0, 0);
-    if (slot[r] >= 0)
-    {
-      const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + row * xs) + lane);
-      v[r] = make_uint4(t[0], t[1], t[2], t[3]);
-    }
+    const int64_t row = row0 + r < n ? row0 + r : n - 1;
+    const u32x4 t = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + row * xs) + lane);
+    v[r] = make_uint4(t[0], t[1], t[2], t[3]);
   }
+  // every slot load issued before any is waited for (clamped rows, masked after)
+  if (slots_i64) {
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) slot[r] = static_cast<const int64_t*>(slots)[row0 + r < n ? row0 + r : n - 1];
+  } else {
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) slot[r] = static_cast<const int32_t*>(slots)[row0 + r < n ? row0 + r : n - 1];
+  }
+#pragma unroll
+  for (int r = 0; r < ROWS; r++)
+    if (row0 + r >= n || slot[r] >= capacity) slot[r] = -1;
 #pragma unroll
   for (int r = 0; r < ROWS; r++) {
     if (slot[r] < 0) continue;  // wave-uniform
