@@ -610,22 +610,27 @@ __device__ void emit_selected(SelShared<kThreads>& sh, const uint32_t (&kk)[P], 
 }
 
 // Keys of row positions i0 + [0, P) (P and i0 multiples of 4); positions at
-// or past n get key 0.  vec: x is 16-byte aligned (rows of a stride that is
-// a multiple of 4 floats), else every key is its own load.
+// or past n get key 0 (n >= 1).  vec: x is 16-byte aligned (rows of a stride
+// that is a multiple of 4 floats).  Every load of the thread is issued before
+// any key is formed: converting each load's value inside its own branch made
+// the compiler wait for it before issuing the next.  A thread whose
+// positions are all valid takes P / 4 16-byte loads; the others (the row's
+// tail) P single loads from positions clamped to n - 1, masked afterwards.
 template <int P>
 __device__ __forceinline__ void load_row_keys(const float* x, int n, int i0, bool vec, uint32_t (&kk)[P]) {
+  float f[P];
+  if (vec && i0 + P <= n) {
 #pragma unroll
-  for (int q = 0; q < P / 4; q++) {
-    const int p = i0 + 4 * q;
-    if (vec && p + 3 < n) {
-      const float4 v = *reinterpret_cast<const float4*>(x + p);
-      kk[4 * q] = order_key(v.x); kk[4 * q + 1] = order_key(v.y);
-      kk[4 * q + 2] = order_key(v.z); kk[4 * q + 3] = order_key(v.w);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; e++) kk[4 * q + e] = p + e < n ? order_key(x[p + e]) : 0u;
+    for (int q = 0; q < P / 4; q++) {
+      const float4 v = *reinterpret_cast<const float4*>(x + i0 + 4 * q);
+      f[4 * q] = v.x; f[4 * q + 1] = v.y; f[4 * q + 2] = v.z; f[4 * q + 3] = v.w;
     }
+  } else {
+#pragma unroll
+    for (int j = 0; j < P; j++) f[j] = x[i0 + j < n ? i0 + j : n - 1];
   }
+#pragma unroll
+  for (int j = 0; j < P; j++) kk[j] = i0 + j < n ? order_key(f[j]) : 0u;
 }
 
 template <int P, class F>
