@@ -10,7 +10,7 @@ from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "libglm53_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EXPORTED = (
     "glm53_abi_version",

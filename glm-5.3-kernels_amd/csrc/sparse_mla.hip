@@ -55,7 +55,6 @@ constexpr int kChunkTiles = 8;         // tiles whose gathers are in flight toge
 constexpr int kRounds = kChunkTiles / kGroups;
 constexpr int kMergeLanes = 8;         // split lanes per output chunk in the LSE merge
 constexpr int kMaxMergeSplits = 1024;
-constexpr int kParkStride = kSlice + 4;  // fp32 per parked row (16 heads x 128 latents per wave): rows 4 banks apart
 constexpr float kNegLarge = -1.0e30f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -231,12 +230,23 @@ __device__ __forceinline__ int pooled_position(PoolAt pool, int num_pools, int p
 // banks; the 16-byte chunks of rows 8-15 of every 16 (row bit 3) are XOR-
 // swapped in pairs so that a 16-byte write of 16 consecutive rows at one
 // column is conflict-free too (without it rows r and r + 8 share banks).
-// Wave w's parked accumulators: its V buffer viewed as 16 rows of
-// kParkStride floats (8448 bytes of the buffer's 9216).
+// Wave w's parked accumulators: its V buffer holding the wave's 8 MFMA
+// accumulator tiles in register order (float4 of lane l of tile dt at
+// (64 dt + l) * 4): each 16-byte write and read instruction covers 1 KB.
 template <class Shared>
 __device__ __forceinline__ float* park_of(Shared& sh, int w) {
-  static_assert(kHeads * kParkStride * 4 <= kTile * kVStride * 2, "a wave's park fits its V buffer");
+  static_assert(8 * 64 * 16 <= kTile * kVStride * 2, "a wave's park fits its V buffer");
   return reinterpret_cast<float*>(&sh.vbuf[w][0][0]);
+}
+
+// Split partials in the accumulator order.  Per (token, split, head group)
+// one block of 16 heads x 512 latents; within it the float4 at
+// ((8 sl + dt) * 64 + 16 g + c) * 4 holds head c, latents 128 sl + 16 dt +
+// 4 g + [0, 4) -- what lane (g, c) of latent slice sl holds in accumulator
+// tile dt -- so every store instruction of a wave writes 1 KB contiguously.
+__device__ __forceinline__ float* part_block(const MlaArgs& a, int t, int split, int hg) {
+  return a.part + ((static_cast<int64_t>(t) * a.num_splits + split) * (a.heads_padded / kHeads) + hg) *
+                      (kHeads * kLatent);
 }
 
 template <class Shared>
@@ -517,113 +527,96 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
   }
 
   // ---- one key group: nothing to merge.  Each wave stores its 16 heads x
-  // 128 latents straight from the MFMA C layout (16 heads x 64-byte pieces
-  // per store instruction), with no LDS round trip and no barrier.
+  // 128 latents straight from its accumulators, with no LDS round trip and
+  // no barrier: the partials are in the accumulator order (1 KB per store
+  // instruction); a single split's bf16 rows take 8 bytes per lane.
   if constexpr (kG == 1) {
     const float inv_l = 1.f / (l_run > 0.f ? l_run : 1.f);
-    if (!head_ok) return;
     const bool direct = a.num_splits == 1 && !a.partials_only;
-    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
+    if (direct) {
+      if (!head_ok) return;
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++) {
-      const float4 v = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l, acc[dt][2] * inv_l, acc[dt][3] * inv_l);
-      const int col = kSlice * sl + 16 * dt + 4 * g;   // head c, latents 128 sl + 16 dt + 4 g + [0, 4)
-      if (direct)
+      for (int dt = 0; dt < 8; dt++) {
+        const int col = kSlice * sl + 16 * dt + 4 * g;   // head c, latents 128 sl + 16 dt + 4 g + [0, 4)
         *reinterpret_cast<uint2*>(a.out + t * a.so_t + head * a.so_h + col) =
-            make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
-      else
-        *reinterpret_cast<float4*>(a.part + row * kLatent + col) = v;
+            make_uint2(pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l),
+                       pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l));
+      }
+      return;
     }
-    if (!direct && sl == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
-    return;
-  } else {
-  // ---- combine the key groups and write the 16 result rows.  The MFMA
-  // C layout scatters a lane's values over 16 rows (16 x 64-byte pieces per
-  // store instruction, which the memory pipeline issues ~2.5x slower than
-  // contiguous ones), so every wave parks its 16 heads x 128 latents
-  // row-major in its own V buffer (which no other wave reads, so parking
-  // waits for nobody), and after one barrier every wave finishes whole rows
-  // with contiguous 1 KB stores.
-  {
-    float* rp = park_of(sh, w) + c * kParkStride + 4 * g;
+    float* pb = part_block(a, t, split, hg) + (8 * sl * 64 + lane) * 4;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
-      *reinterpret_cast<float4*>(rp + 16 * dt) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
-    if (sl == 0 && g == 0) {
-      sh.ml[kg][c][0] = m_run;
-      sh.ml[kg][c][1] = l_run;
-    }
+      *reinterpret_cast<float4*>(pb + dt * 64 * 4) =
+          make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l, acc[dt][2] * inv_l, acc[dt][3] * inv_l);
+    if (head_ok && sl == 0 && g == 0)
+      a.lse[(static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head] = (m_run + log2f(l_run)) * kLn2;
+    return;
+  } else {
+  // ---- combine the key groups.  Accumulator tile dt of every slice belongs
+  // to key group dt * kG / 8 (3-3-2 tiles for three groups, 4-4 for two):
+  // each wave parks the tiles that other groups own in its V buffer (register
+  // order, 1 KB per instruction) and writes its (m, l); after one barrier
+  // every wave adds the other groups' parked copies of its own tiles to its
+  // registers, in group order (x0 a0 + x1 a1) + x2 a2, and stores them
+  // straight from registers in the partials' accumulator order (1 KB per
+  // instruction; a single split's bf16 rows take 8 bytes per lane).
+  auto owner = [](int dt) { return dt * kG / 8; };
+  {
+    float* pk = park_of(sh, w) + 4 * lane;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+      if (owner(dt) != kg)
+        *reinterpret_cast<float4*>(pk + dt * 64 * 4) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+  }
+  if (sl == 0 && g == 0) {
+    sh.ml[kg][c][0] = m_run;
+    sh.ml[kg][c][1] = l_run;
   }
   __syncthreads();
-  constexpr int kRowsPerWave = (kHeads + kWaves - 1) / kWaves;
+  float mg[kG], ag[kG];
+  float mm = kNegLarge;
 #pragma unroll
-  for (int k = 0; k < kRowsPerWave; k++) {
-    // result row (head in the group), uniform per wave: consecutive rows per
-    // wave when they divide evenly, else dealt round robin
-    const int r = kHeads % kWaves == 0 ? kRowsPerWave * w + k : w + kWaves * k;
-    const int hd = hg * kHeads + r;
-    if (r >= kHeads || hd >= a.num_heads) break;
-    float mg[kG], ag[kG];
-    float mm = kNegLarge;
+  for (int i = 0; i < kG; i++) {
+    mg[i] = sh.ml[i][c][0];
+    mm = i == 0 ? mg[0] : fmaxf(mm, mg[i]);
+  }
+  float l = 0.f;
+#pragma unroll
+  for (int i = 0; i < kG; i++) {
+    ag[i] = fast_exp2(mg[i] - mm);
+    const float li = sh.ml[i][c][1] * ag[i];
+    l = i == 0 ? li : l + li;
+  }
+  // 1 / l once, then multiplies (the reference divides; the two differ by
+  // at most one fp32 ulp before the bf16 / fp32 store).
+  const float inv_l = 1.f / (l > 0.f ? l : 1.f);
+  const bool direct = a.num_splits == 1 && !a.partials_only;
+  float* pb = part_block(a, t, split, hg) + (8 * sl * 64 + lane) * 4;
+#pragma unroll
+  for (int dt = 0; dt < 8; dt++) {
+    if (owner(dt) != kg) continue;   // uniform across the wave
+    float4 v;
 #pragma unroll
     for (int i = 0; i < kG; i++) {
-      mg[i] = sh.ml[i][r][0];
-      mm = i == 0 ? mg[0] : fmaxf(mm, mg[i]);
+      const float4 x = i == kg ? make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3])
+                               : *reinterpret_cast<const float4*>(park_of(sh, i * kSlices + sl) + (dt * 64 + lane) * 4);
+      v = i == 0 ? make_float4(x.x * ag[0], x.y * ag[0], x.z * ag[0], x.w * ag[0])
+                 : make_float4(v.x + x.x * ag[i], v.y + x.y * ag[i], v.z + x.z * ag[i], v.w + x.w * ag[i]);
     }
-    float l = 0.f;
-#pragma unroll
-    for (int i = 0; i < kG; i++) {
-      ag[i] = fast_exp2(mg[i] - mm);
-      const float li = sh.ml[i][r][1] * ag[i];
-      l = i == 0 ? li : l + li;
-    }
-    // 1 / l once, then multiplies (the reference divides; the two differ by
-    // at most one fp32 ulp before the bf16 / fp32 store).
-    const float inv_l = 1.f / (l > 0.f ? l : 1.f);
-    // key groups added in order: (x0 a0 + x1 a1) + x2 a2
-    // latent col of head r for key group i: in the park of wave (i, col / 128)
-    auto parked = [&](int i, int col) {
-      return *reinterpret_cast<const float4*>(park_of(sh, i * kSlices + col / kSlice) + r * kParkStride +
-                                              col % kSlice);
-    };
-    auto fin4 = [&](int col) {
-      float4 v = parked(0, col);
-      v = make_float4(v.x * ag[0], v.y * ag[0], v.z * ag[0], v.w * ag[0]);
-#pragma unroll
-      for (int i = 1; i < kG; i++) {
-        const float4 x = parked(i, col);
-        v = make_float4(v.x + x.x * ag[i], v.y + x.y * ag[i], v.z + x.z * ag[i], v.w + x.w * ag[i]);
-      }
-      return make_float4(v.x * inv_l, v.y * inv_l, v.z * inv_l, v.w * inv_l);
-    };
-    if (a.num_splits == 1 && !a.partials_only) {
-      // lane: latents [8 lane, 8 lane + 8) -> one 16-byte bf16 store
-      const float4 u = fin4(8 * lane);
-      const float4 v = fin4(8 * lane + 4);
-      uint4 o;
-      o.x = pack_bf16x2(u.x, u.y);
-      o.y = pack_bf16x2(u.z, u.w);
-      o.z = pack_bf16x2(v.x, v.y);
-      o.w = pack_bf16x2(v.z, v.w);
-      uint16_t* op = a.out + t * a.so_t + hd * a.so_h + 8 * lane;
-      if (a.out_align16) {
-        *reinterpret_cast<uint4*>(op) = o;
-      } else {
-        reinterpret_cast<uint2*>(op)[0] = make_uint2(o.x, o.y);
-        reinterpret_cast<uint2*>(op)[1] = make_uint2(o.z, o.w);
-      }
+    v = make_float4(v.x * inv_l, v.y * inv_l, v.z * inv_l, v.w * inv_l);
+    if (direct) {
+      const int col = kSlice * sl + 16 * dt + 4 * g;   // head c, latents 128 sl + 16 dt + 4 g + [0, 4)
+      if (head_ok)
+        *reinterpret_cast<uint2*>(a.out + t * a.so_t + head * a.so_h + col) =
+            make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
     } else {
-      const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + hd;
-      float* pp = a.part + row * kLatent;
-      // Streaming stores: the merge kernel reads each partial once (B=8
-      // step -0.2 us against plain stores; the one-key-group kernel's
-      // 64-byte C-layout pieces keep plain stores).
-      const float4 f0 = fin4(4 * lane), f1 = fin4(256 + 4 * lane);
-      __builtin_nontemporal_store(f32x4{f0.x, f0.y, f0.z, f0.w}, reinterpret_cast<f32x4*>(pp + 4 * lane));
-      __builtin_nontemporal_store(f32x4{f1.x, f1.y, f1.z, f1.w}, reinterpret_cast<f32x4*>(pp + 256 + 4 * lane));
-      if (lane == 0) a.lse[row] = (mm + log2f(l)) * kLn2;
+      // streaming stores: the merge kernel reads each partial once
+      __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(pb + dt * 64 * 4));
     }
   }
+  if (!direct && head_ok && kg == 0 && sl == 0 && g == 0)
+    a.lse[(static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head] = (mm + log2f(l)) * kLn2;
   }
 }
 
@@ -925,13 +918,14 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
       *reinterpret_cast<uint2*>(op + 16 * dt) = make_uint2(pack_bf16x2(acc[dt][0] * inv_l, acc[dt][1] * inv_l),
                                                            pack_bf16x2(acc[dt][2] * inv_l, acc[dt][3] * inv_l));
   } else {
-    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
-    float* pp = a.part + row * kLatent + kHalfLat * w + 4 * g;
+    // accumulator order: latents 256 w + 16 dt + 4 g are slice 2 w + dt / 8, tile dt % 8
+    float* pb = part_block(a, t, split, hg) + (16 * w * 64 + lane) * 4;
 #pragma unroll
     for (int dt = 0; dt < 16; dt++)
-      *reinterpret_cast<float4*>(pp + 16 * dt) = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l,
-                                                             acc[dt][2] * inv_l, acc[dt][3] * inv_l);
-    if (w == 0 && g == 0) a.lse[row] = (m_run + log2f(l_run)) * kLn2;
+      *reinterpret_cast<float4*>(pb + dt * 64 * 4) = make_float4(acc[dt][0] * inv_l, acc[dt][1] * inv_l,
+                                                                 acc[dt][2] * inv_l, acc[dt][3] * inv_l);
+    if (w == 0 && g == 0)
+      a.lse[(static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head] = (m_run + log2f(l_run)) * kLn2;
   }
 }
 
@@ -944,7 +938,6 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
 // softmax add to.
 template <int kG>
 __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_floor_kernel(const MlaArgs a) {
-  constexpr int kWaves = SplitShape<kG>::kWaves;
   constexpr int kRounds = SplitShape<kG>::kRounds;
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
   if ((gridDim.y * gridDim.z) % 8 == 0) {
@@ -1008,29 +1001,16 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
       fold ^= kd[r][u][0].x ^ kd[r][u][0].y ^ kd[r][u][0].z ^ kd[r][u][0].w ^
               kd[r][u][1].x ^ kd[r][u][1].y ^ kd[r][u][1].z ^ kd[r][u][1].w;
   }
-  // a finite float from the folded bits, stored where and as the split kernel stores
+  // a finite float from the folded bits, stored where and as the split
+  // kernel stores: each wave its key group's accumulator tiles (tile dt of
+  // group dt * kG / 8), 1 KB per instruction in the accumulator order
   const float x = static_cast<float>(fold & 0xffff);
-  if constexpr (kG == 1) {   // straight from the C layout: head c, latents 128 sl + 16 dt + 4 g + [0, 4)
-    if (head >= a.num_heads) return;
-    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head;
+  float* pb = part_block(a, t, split, hg) + (8 * sl * 64 + lane) * 4;
 #pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-      *reinterpret_cast<float4*>(a.part + row * kLatent + kSlice * sl + 16 * dt + 4 * g) = make_float4(x, x, x, x);
-    if (sl == 0 && g == 0) a.lse[row] = x;
-    return;
-  }
-  constexpr int kRowsPerWave = (kHeads + kWaves - 1) / kWaves;
-#pragma unroll
-  for (int k = 0; k < kRowsPerWave; k++) {
-    const int r = kHeads % kWaves == 0 ? kRowsPerWave * w + k : w + kWaves * k;   // as the split kernel
-    const int hd = hg * kHeads + r;
-    if (r >= kHeads || hd >= a.num_heads) break;
-    const int64_t row = (static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + hd;
-    float* pp = a.part + row * kLatent;
-    *reinterpret_cast<float4*>(pp + 4 * lane) = make_float4(x, x, x, x);
-    *reinterpret_cast<float4*>(pp + 256 + 4 * lane) = make_float4(x, x, x, x);
-    if (lane == 0) a.lse[row] = x;
-  }
+  for (int dt = 0; dt < 8; dt++)
+    if (dt * kG / 8 == kg) *reinterpret_cast<float4*>(pb + dt * 64 * 4) = make_float4(x, x, x, x);
+  if (head < a.num_heads && kg == 0 && sl == 0 && g == 0)
+    a.lse[(static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head] = x;
 }
 
 // Standalone conversion (the vLLM helper the reference's adapter calls):
@@ -1075,40 +1055,49 @@ __global__ __launch_bounds__(256) void expand_pools_kernel(const PoolT* __restri
 }
 
 // N-way LSE merge (kernels/titan_mla.py:403-429).  One workgroup per
-// (token, head, 128-latent quarter); 256 threads = 8 split lanes x 32 chunks
-// of 4 latents.  Split lane k handles splits k, k + 8, ...: it loads their
-// partials and LSEs together (one memory round trip), the block takes the
-// maximum M of all LSEs, and each lane accumulates sum e^{lse_s - M} part_s
-// and sum e^{lse_s - M} over its splits in order; the 8 lanes are then summed
-// in a fixed order.  out = acc / den: the reference's running rescaled sum
+// (token, head group, 16-latent tile of the accumulator order: slice sl,
+// tile dt); 512 threads = 8 split lanes x 64 positions, position p = 16 g +
+// c holding head c, latents 128 sl + 16 dt + 4 g + [0, 4) -- each split's
+// 1 KB block of the tile is one contiguous load per split lane.  Split lane
+// k handles splits k, k + 8, ...: it loads their partials and LSEs together
+// (one memory round trip), the block takes the maximum M of the head's
+// LSEs, and each lane accumulates sum e^{lse_s - M} part_s and
+// sum e^{lse_s - M} over its splits in order; the 8 lanes are then summed in
+// a fixed order.  out = acc / den: the reference's running rescaled sum
 // written without a serial dependency, deterministic.  Empty splits carry
 // lse = -inf and weigh 0; no valid split gives 0.
 constexpr int kMergeRegs = 16;   // splits per lane held in registers (S <= 128)
+constexpr int kMergeThreads = kMergeLanes * 64;
 
-__global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __restrict__ part,
-                                                               const float* __restrict__ lse,
-                                                               int num_splits, int heads_padded,
-                                                               int num_heads,
-                                                               uint16_t* __restrict__ out,
-                                                               int64_t so_t, int64_t so_h) {
-  __shared__ float red_m[256 / 64];
-  __shared__ float part_den[kMergeLanes];
-  __shared__ __attribute__((aligned(16))) float4 part_sum[kMergeLanes][32];
+__global__ __launch_bounds__(kMergeThreads) void sparse_mla_merge_kernel(const float* __restrict__ part,
+                                                                          const float* __restrict__ lse,
+                                                                          int num_splits, int heads_padded,
+                                                                          int num_heads,
+                                                                          uint16_t* __restrict__ out,
+                                                                          int64_t so_t, int64_t so_h) {
+  __shared__ float red_m[kMergeLanes][64];
+  __shared__ float part_den[kMergeLanes][64];
+  __shared__ __attribute__((aligned(16))) float4 part_sum[kMergeLanes][64];
   // token fastest in the linear id: with a multiple of 8 tokens, token t's
   // workgroups share the XCD that ran its splits
-  const int num_tokens = gridDim.x / num_heads;
-  int t = blockIdx.x / num_heads, h = blockIdx.x % num_heads, quarter = blockIdx.y;
+  const int groups = heads_padded / kHeads;
+  const int num_tokens = gridDim.x / groups;
+  int t = blockIdx.x / groups, hg = blockIdx.x % groups, tile = blockIdx.y;
   if (num_tokens % 8 == 0) {
     const int lin = blockIdx.x + gridDim.x * blockIdx.y;
     t = lin % num_tokens;
-    h = (lin / num_tokens) % num_heads;
-    quarter = lin / (num_tokens * num_heads);
+    hg = (lin / num_tokens) % groups;
+    tile = lin / (num_tokens * groups);
   }
   const int tid = threadIdx.x;
-  const int sl = tid >> 5;          // split lane
-  const int ch = tid & 31;          // 4-latent chunk in the quarter
-  const int64_t row0 = static_cast<int64_t>(t) * num_splits * heads_padded + h;
-  const int d = quarter * 128 + ch * 4;
+  const int sp = tid >> 6;          // split lane (one wave each)
+  const int p = tid & 63;           // position 16 g + c
+  const int head = hg * kHeads + (p & 15);
+  // split s: block (t * S + s) * groups + hg, float4 tile * 64 + p in it
+  const int64_t blk0 = static_cast<int64_t>(t) * num_splits * groups + hg;
+  const int64_t blk_stride = static_cast<int64_t>(groups) * kHeads * kLatent;
+  const float* pp = part + blk0 * kHeads * kLatent + (tile * 64 + p) * 4;
+  const float* lp = lse + static_cast<int64_t>(t) * num_splits * heads_padded + head;
   const bool in_regs = num_splits <= kMergeLanes * kMergeRegs;
 
   float4 pv[kMergeRegs];
@@ -1117,31 +1106,28 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
   if (in_regs) {
 #pragma unroll
     for (int j = 0; j < kMergeRegs; j++) {
-      const int s = sl + kMergeLanes * j;
-      const int64_t r = row0 + static_cast<int64_t>(s) * heads_padded;
+      const int s = sp + kMergeLanes * j;
       f32x4 x = f32x4{0.f, 0.f, 0.f, 0.f};   // read once: streaming loads
-      if (s < num_splits) x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(part + r * kLatent + d));
+      if (s < num_splits) x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(pp + s * blk_stride));
       pv[j] = make_float4(x[0], x[1], x[2], x[3]);
-      lv[j] = s < num_splits ? lse[r] : kNegLarge;
+      lv[j] = s < num_splits ? lp[static_cast<int64_t>(s) * heads_padded] : kNegLarge;
     }
 #pragma unroll
     for (int j = 0; j < kMergeRegs; j++) m = fmaxf(m, lv[j]);
   } else {
-    for (int s = sl; s < num_splits; s += kMergeLanes)
-      m = fmaxf(m, lse[row0 + static_cast<int64_t>(s) * heads_padded]);
+    for (int s = sp; s < num_splits; s += kMergeLanes) m = fmaxf(m, lp[static_cast<int64_t>(s) * heads_padded]);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  if ((tid & 63) == 0) red_m[tid >> 6] = m;
+  red_m[sp][p] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+#pragma unroll
+  for (int k = 0; k < kMergeLanes; k++) m = fmaxf(m, red_m[k][p]);
 
   float den = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (in_regs) {
 #pragma unroll
     for (int j = 0; j < kMergeRegs; j++) {
-      if (sl + kMergeLanes * j < num_splits) {
+      if (sp + kMergeLanes * j < num_splits) {
         const float e = expf(lv[j] - m);
         acc.x += e * pv[j].x;
         acc.y += e * pv[j].y;
@@ -1151,10 +1137,9 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
       }
     }
   } else {
-    for (int s = sl; s < num_splits; s += kMergeLanes) {
-      const int64_t r = row0 + static_cast<int64_t>(s) * heads_padded;
-      const float e = expf(lse[r] - m);
-      const float4 v = *reinterpret_cast<const float4*>(part + r * kLatent + d);
+    for (int s = sp; s < num_splits; s += kMergeLanes) {
+      const float e = expf(lp[static_cast<int64_t>(s) * heads_padded] - m);
+      const float4 v = *reinterpret_cast<const float4*>(pp + s * blk_stride);
       acc.x += e * v.x;
       acc.y += e * v.y;
       acc.z += e * v.z;
@@ -1162,23 +1147,24 @@ __global__ __launch_bounds__(256) void sparse_mla_merge_kernel(const float* __re
       den += e;
     }
   }
-  part_sum[sl][ch] = acc;
-  if (ch == 0) part_den[sl] = den;
+  part_sum[sp][p] = acc;
+  part_den[sp][p] = den;
   __syncthreads();
-  if (sl == 0) {
-    float4 r = part_sum[0][ch];
-    float dsum = part_den[0];
+  if (sp == 0 && head < num_heads) {
+    float4 r = part_sum[0][p];
+    float dsum = part_den[0][p];
 #pragma unroll
     for (int k = 1; k < kMergeLanes; k++) {
-      const float4 v = part_sum[k][ch];
+      const float4 v = part_sum[k][p];
       r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
-      dsum += part_den[k];
+      dsum += part_den[k][p];
     }
     const float inv = 1.f / (dsum > 0.f ? dsum : 1.f);
     uint2 o;
     o.x = pack_bf16x2(r.x * inv, r.y * inv);
     o.y = pack_bf16x2(r.z * inv, r.w * inv);
-    *reinterpret_cast<uint2*>(out + t * so_t + h * so_h + d) = o;
+    const int d = kSlice * (tile >> 3) + 16 * (tile & 7) + 4 * (p >> 4);
+    *reinterpret_cast<uint2*>(out + t * so_t + head * so_h + d) = o;
   }
 }
 
@@ -1280,8 +1266,8 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
 void launch_merge(const float* part, const float* lse, int64_t num_tokens, int num_splits,
                   int heads_padded, int num_heads, uint16_t* out, int64_t so_t, int64_t so_h,
                   hipStream_t st) {
-  hipLaunchKernelGGL(sparse_mla_merge_kernel, dim3(static_cast<unsigned>(num_tokens * num_heads), 4),
-                     dim3(256), 0, st, part, lse, num_splits, heads_padded, num_heads, out, so_t, so_h);
+  hipLaunchKernelGGL(sparse_mla_merge_kernel, dim3(static_cast<unsigned>(num_tokens * (heads_padded / kHeads)), 32),
+                     dim3(kMergeThreads), 0, st, part, lse, num_splits, heads_padded, num_heads, out, so_t, so_h);
 }
 
 }  // namespace

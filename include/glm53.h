@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define GLM53_ABI_VERSION 2
+#define GLM53_ABI_VERSION 3
 
 /* Argument errors (negative return codes). */
 #define GLM53_ERR_NULL_POINTER   (-1)
@@ -199,9 +199,15 @@ int glm53_sparse_mla_pooled(const void* q, int64_t sq_t, int64_t sq_h,
  *
  * Partials layout (fp32), rows = num_tokens * num_splits * Hp with
  * Hp = num_heads rounded up to a multiple of 16, row r = (t * num_splits +
- * s) * Hp + h:
- *   part[rows][512]  normalised split output acc / l  (0 for an empty split)
- *   lse[rows]        (m + log2 l) * ln 2, natural-log LSE (-inf when empty)
+ * s) * Hp + h, head group hg = h / 16, c = h % 16:
+ *   part[rows * 512]  normalised split output acc / l  (0 for an empty split),
+ *                     in blocks of 16 heads x 512 latents per (t, s, hg) at
+ *                     ((t * num_splits + s) * Hp / 16 + hg) * 8192 floats;
+ *                     within a block, latent d of head c is float
+ *                     ((8 * (d / 128) + d % 128 / 16) * 64 + 16 * (d % 16 / 4)
+ *                     + c) * 4 + d % 4 (the MFMA accumulator order of the
+ *                     kernels, so that each store instruction writes 1 KB)
+ *   lse[rows]         (m + log2 l) * ln 2, natural-log LSE (-inf when empty)
  * glm53_sparse_mla_partials writes them for any num_splits >= 1;
  * glm53_sparse_mla_merge combines them into bf16 out with log-sum-exp
  * weights.  glm53_sparse_mla_partials_bytes gives the buffer size.

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_glm53_lib.EXPORTED)
     for n in names:
         assert hasattr(lib, n), n
-    assert lib.glm53_abi_version() == 2
+    assert lib.glm53_abi_version() == 3
 
 
 def test_host_side_argument_errors():
