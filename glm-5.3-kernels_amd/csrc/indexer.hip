@@ -422,6 +422,15 @@ struct SelShared {
   uint32_t pick[3];              // digit, keys above it, keys in it
 };
 
+// Zero both histograms.  Callers issue it while their keys' loads are in
+// flight; the first barrier of radix_threshold orders it before the first
+// atomics.
+template <int kThreads>
+__device__ __forceinline__ void clear_hist(SelShared<kThreads>& sh) {
+  for (int b = threadIdx.x; b < 2 * kHistBins / 4; b += kThreads)
+    reinterpret_cast<uint4*>(&sh.hist[0][0])[b] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 // Inclusive scan of one value per lane within the wave: row_shr 1, 2, 4, 8
 // inside rows of 16 lanes, then row_bcast 15 and 31 carry row totals upward.
 template <int kCtrl, int kRowMask>
@@ -485,7 +494,8 @@ struct Threshold {
 // concentrated set of keys (a chunk's candidates) still spreads over the
 // bins, which keeps the histogram atomics from piling onto a few addresses.
 // for_keys(f) calls f(key) for every key of this thread; the keys matching
-// the shared bits must number at least k.
+// the shared bits must number at least k.  The caller has zeroed both
+// histograms (clear_hist) before the call.
 template <int kThreads, class ForKeys>
 __device__ Threshold radix_threshold(SelShared<kThreads>& sh, ForKeys for_keys, uint32_t k, uint32_t kmin,
                                      uint32_t kmax) {
@@ -494,8 +504,7 @@ __device__ Threshold radix_threshold(SelShared<kThreads>& sh, ForKeys for_keys, 
   kmin = ~wave_max(~kmin);
   kmax = wave_max(kmax);
   if (lane == 0) { sh.wmin[w] = kmin; sh.wmax[w] = kmax; }
-  for (int b = tid; b < 2 * kHistBins; b += kThreads) (&sh.hist[0][0])[b] = 0u;
-  __syncthreads();
+  __syncthreads();   // also orders the caller's clear_hist before the first atomics
 #pragma unroll
   for (int i = 0; i < kWaves; i++) { kmin = min(kmin, sh.wmin[i]); kmax = max(kmax, sh.wmax[i]); }
   const uint32_t diff = kmin ^ kmax;
@@ -514,7 +523,8 @@ __device__ Threshold radix_threshold(SelShared<kThreads>& sh, ForKeys for_keys, 
       if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & dmask], 1u);
     });
     if (pass == 1)   // pass 0's histogram is no longer read: clear it for pass 2
-      for (int b = tid; b < kHistBins; b += kThreads) sh.hist[0][b] = 0u;
+      for (int b = tid; b < kHistBins / 4; b += kThreads)
+        reinterpret_cast<uint4*>(sh.hist[0])[b] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     // Thread tid owns bpt bins counted from the top (held in registers): the
     // keys in higher bins are the wave totals of lower waves plus the lanes
@@ -617,8 +627,7 @@ __device__ void emit_selected(SelShared<kThreads>& sh, const uint32_t (&kk)[P], 
 // positions are all valid takes P / 4 16-byte loads; the others (the row's
 // tail) P single loads from positions clamped to n - 1, masked afterwards.
 template <int P>
-__device__ __forceinline__ void load_row_keys(const float* x, int n, int i0, bool vec, uint32_t (&kk)[P]) {
-  float f[P];
+__device__ __forceinline__ void issue_row_loads(const float* x, int n, int i0, bool vec, float (&f)[P]) {
   if (vec && i0 + P <= n) {
 #pragma unroll
     for (int q = 0; q < P / 4; q++) {
@@ -629,8 +638,19 @@ __device__ __forceinline__ void load_row_keys(const float* x, int n, int i0, boo
 #pragma unroll
     for (int j = 0; j < P; j++) f[j] = x[i0 + j < n ? i0 + j : n - 1];
   }
+}
+
+template <int P>
+__device__ __forceinline__ void form_keys(const float (&f)[P], int n, int i0, uint32_t (&kk)[P]) {
 #pragma unroll
   for (int j = 0; j < P; j++) kk[j] = i0 + j < n ? order_key(f[j]) : 0u;
+}
+
+template <int P>
+__device__ __forceinline__ void load_row_keys(const float* x, int n, int i0, bool vec, uint32_t (&kk)[P]) {
+  float f[P];
+  issue_row_loads<P>(x, n, i0, vec, f);
+  form_keys<P>(f, n, i0, kk);
 }
 
 template <int P, class F>
@@ -658,8 +678,11 @@ __global__ __launch_bounds__(kChunkThreads) void topk_chunk_kernel(const TopkArg
   const int rest = len - start;
   const int valid = rest < 0 ? 0 : rest > a.chunk_len ? a.chunk_len : rest;
   if (len <= k || valid == 0) return;   // uniform
+  float f[P];
+  issue_row_loads<P>(a.logits + row * a.sl + start, valid, tid * P, a.vec, f);
+  if (valid > k) clear_hist(sh);   // under the loads' latency (uniform)
   uint32_t kk[P];
-  load_row_keys<P>(a.logits + row * a.sl + start, valid, tid * P, a.vec, kk);
+  form_keys<P>(f, valid, tid * P, kk);
   const int64_t cb = (static_cast<int64_t>(row) * a.chunks + c) * k;
   uint32_t* ck = a.cand_key + cb;
   int32_t* cp = a.cand_pos + cb;
@@ -710,13 +733,17 @@ __global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(const TopkArg
     // k is not a multiple of 4, else as 4-candidate vectors (a vector never
     // straddles chunks then); filled slots are picked afterwards.
     const int n_cand = a.chunks * k;
-    if ((k & 3) == 0) {
+    if ((k & 3) == 0) {   // keys first: the first pass waits for them only
 #pragma unroll
       for (int q = 0; q < P / 4; q++) {
         const int i = tid * P + 4 * q < n_cand ? tid * P + 4 * q : n_cand - 4;
         const uint4 kv = *reinterpret_cast<const uint4*>(a.cand_key + cb + i);
-        const int4 pv = *reinterpret_cast<const int4*>(a.cand_pos + cb + i);
         kk[4 * q] = kv.x; kk[4 * q + 1] = kv.y; kk[4 * q + 2] = kv.z; kk[4 * q + 3] = kv.w;
+      }
+#pragma unroll
+      for (int q = 0; q < P / 4; q++) {
+        const int i = tid * P + 4 * q < n_cand ? tid * P + 4 * q : n_cand - 4;
+        const int4 pv = *reinterpret_cast<const int4*>(a.cand_pos + cb + i);
         pos[4 * q] = pv.x; pos[4 * q + 1] = pv.y; pos[4 * q + 2] = pv.z; pos[4 * q + 3] = pv.w;
       }
     } else {
@@ -727,6 +754,7 @@ __global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(const TopkArg
         pos[j] = a.cand_pos[cb + i];
       }
     }
+    clear_hist(sh);   // under the loads' latency
     int c = (tid * P) / k, sl = tid * P - c * k;
 #pragma unroll
     for (int j = 0; j < P; j++) {
@@ -738,7 +766,10 @@ __global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(const TopkArg
       if (++sl == k) { sl = 0; c++; }
     }
   } else {
-    load_row_keys<P>(a.logits + row * a.sl, len, tid * P, a.vec, kk);
+    float f[P];
+    issue_row_loads<P>(a.logits + row * a.sl, len, tid * P, a.vec, f);
+    clear_hist(sh);   // under the loads' latency
+    form_keys<P>(f, len, tid * P, kk);
 #pragma unroll
     for (int j = 0; j < P; j++)
       if (tid * P + j < len) { kmin = min(kmin, kk[j]); kmax = max(kmax, kk[j]); }
@@ -765,6 +796,7 @@ __global__ __launch_bounds__(kSweepThreads) void topk_sweep_kernel(const TopkArg
   }
   const float* x = a.logits + row * a.sl;
   const int sweeps = (len + kSweep - 1) / kSweep;
+  clear_hist(sh);
   const Threshold t = radix_threshold(sh, [&](auto f) {
     for (int sw = 0; sw < sweeps; sw++) {
       uint32_t kk[kSweepKeys];
