@@ -668,9 +668,9 @@ __device__ __forceinline__ int clamp_len(const TopkArgs& a, int row) {
 // [c * chunk_len, (c + 1) * chunk_len) of the row, in position order, as
 // candidates (every valid position when the chunk holds at most k).  A key of
 // the row's top k is in its chunk's top k, so the candidates hold the answer.
-template <int P>
-__global__ __launch_bounds__(kChunkThreads) void topk_chunk_kernel(const TopkArgs a) {
-  __shared__ SelShared<kChunkThreads> sh;
+template <int P, int kThreads>
+__global__ __launch_bounds__(kThreads) void topk_chunk_kernel(const TopkArgs a) {
+  __shared__ SelShared<kThreads> sh;
   const int row = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int len = clamp_len(a, row);
   const int k = a.k;
@@ -923,16 +923,21 @@ namespace {
 
 // How the top-k of rows of max_len columns runs: one final workgroup over
 // the row (direct, P keys per thread), or the chunk stage (chunks of
-// 512 * chunk_p positions, chunk_len > k) then the final stage over
-// chunks * k candidates, or the sweep kernel.  For a few rows (latency) the
-// chunk size with the fewest keys per thread over the two stages wins; from
-// 32 rows on (throughput: the chunk stage alone is many workgroups per CU)
-// 8192-position chunks, half the workgroups and candidates (2048 rows x
-// 65536 positions, k = 512: 283 -> 242 us; 32 rows 16.6 -> 15.6 us; 16 rows
-// 15.0 -> 15.5 us, so the latency choice stays below 32).
+// chunk_threads * chunk_p positions, chunk_len > k; 512 threads x 8, 16 or
+// 32 keys, or 1024 threads x 8) then the final stage over chunks * k
+// candidates, or the sweep kernel.  For a few rows (latency) the chunking
+// with the fewest keys per thread over the two stages wins, the first listed
+// on a tie: at 65536 positions and k = 512, 1024-thread workgroups over
+// 8192-position chunks (4096 candidates) rather than 512 over 4096 (8192
+// candidates): B=8 16.4 -> 15.6 us, B=1 11.75 -> 11.66 us.  From 32 rows on
+// (throughput: the chunk stage alone is many workgroups per CU) 512-thread
+// workgroups over 8192-position chunks, half the workgroups and candidates
+// of 4096 (2048 rows x 65536 positions, k = 512: 283 -> 242 us; 32 rows
+// 16.6 -> 15.6 us; 16 rows 15.0 -> 15.5 us, so the latency choice stays
+// below 32).
 struct TopkPlan {
   enum Mode { kDirect, kChunked, kSweepMode } mode;
-  int chunk_p, final_p, chunks, chunk_len;
+  int chunk_p, final_p, chunks, chunk_len, chunk_threads;
 };
 
 int final_p_for(int64_t n) {
@@ -944,25 +949,30 @@ int final_p_for(int64_t n) {
 constexpr int64_t kTopkThroughputRows = 32;
 
 TopkPlan plan_topk(int64_t num_rows, int64_t max_len, int64_t k) {
-  if (max_len <= int64_t(kFinalThreads) * 4) return {TopkPlan::kDirect, 0, 4, 0, 0};
-  TopkPlan best{TopkPlan::kSweepMode, 0, 0, 0, 0};
+  if (max_len <= int64_t(kFinalThreads) * 4) return {TopkPlan::kDirect, 0, 4, 0, 0, 0};
+  TopkPlan best{TopkPlan::kSweepMode, 0, 0, 0, 0, 0};
   int best_cost = 1 << 30;
-  for (int p : {8, 16, 32}) {
-    const int64_t len_c = int64_t(kChunkThreads) * p;
-    if (len_c <= k) continue;
-    const int64_t chunks = (max_len + len_c - 1) / len_c;
-    if (chunks < 2) continue;
-    const int fp = final_p_for(chunks * k);
-    if (fp == 0) continue;
-    const int cost = num_rows >= kTopkThroughputRows && p == 16 ? 0 : p + fp;
-    if (cost < best_cost) {
-      best_cost = cost;
-      best = {TopkPlan::kChunked, p, fp, static_cast<int>(chunks), static_cast<int>(len_c)};
+  for (int threads : {kChunkThreads, kFinalThreads}) {
+    for (int p : {8, 16, 32}) {
+      if (threads == kFinalThreads && p != 8) continue;
+      const int64_t len_c = int64_t(threads) * p;
+      if (len_c <= k) continue;
+      const int64_t chunks = (max_len + len_c - 1) / len_c;
+      if (chunks < 2) continue;
+      const int fp = final_p_for(chunks * k);
+      if (fp == 0) continue;
+      const bool throughput = num_rows >= kTopkThroughputRows;
+      if (throughput && threads != kChunkThreads) continue;
+      const int cost = throughput && p == 16 ? 0 : p + fp;
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = {TopkPlan::kChunked, p, fp, static_cast<int>(chunks), static_cast<int>(len_c), threads};
+      }
     }
   }
   if (best.mode == TopkPlan::kSweepMode) {
     const int fp = final_p_for(max_len);
-    if (fp) return {TopkPlan::kDirect, 0, fp, 0, 0};
+    if (fp) return {TopkPlan::kDirect, 0, fp, 0, 0, 0};
   }
   return best;
 }
@@ -1015,10 +1025,12 @@ extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t
   const bool cand = plan.mode == TopkPlan::kChunked;
   if (cand) {
     const dim3 grid(static_cast<unsigned>(num_rows), static_cast<unsigned>(plan.chunks));
-    switch (plan.chunk_p) {
-      case 8: hipLaunchKernelGGL(topk_chunk_kernel<8>, grid, dim3(kChunkThreads), 0, st, a); break;
-      case 16: hipLaunchKernelGGL(topk_chunk_kernel<16>, grid, dim3(kChunkThreads), 0, st, a); break;
-      default: hipLaunchKernelGGL(topk_chunk_kernel<32>, grid, dim3(kChunkThreads), 0, st, a); break;
+    if (plan.chunk_threads == kFinalThreads)
+      hipLaunchKernelGGL((topk_chunk_kernel<8, kFinalThreads>), grid, dim3(kFinalThreads), 0, st, a);
+    else switch (plan.chunk_p) {
+      case 8: hipLaunchKernelGGL((topk_chunk_kernel<8, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
+      case 16: hipLaunchKernelGGL((topk_chunk_kernel<16, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
+      default: hipLaunchKernelGGL((topk_chunk_kernel<32, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
     }
   }
   switch (plan.final_p) {

@@ -330,7 +330,8 @@ def test_indexer_host_errors():
     # long rows run in two stages and need the candidates' workspace
     ws = L.glm53_indexer_topk_workspace_bytes
     assert ws(8, 4096, 512) == 0
-    assert ws(8, 65536, 512) == 8 * 16 * 512 * 8          # 16 chunks of 4096, key + position per candidate
+    assert ws(8, 65536, 512) == 8 * 8 * 512 * 8           # 8 chunks of 8192, key + position per candidate
+    assert ws(8, 16384, 512) == 8 * 4 * 512 * 8           # 4 chunks of 4096
     assert ws(8, 65536, 2048) == 8 * 8 * 2048 * 8         # 8 chunks of 8192
     assert ws(2, 140000, 4096) == 0                       # too many candidates: single-workgroup sweeps
     assert ws(8, 65536, 0) == 0 and ws(-1, 65536, 512) == 0
@@ -364,7 +365,7 @@ def test_indexer_contract_errors_on_cpu():
 
 def test_topk_plans_keep_their_invariants():
     """The two-stage top-k's plan (through the workspace size it needs): when
-    it chunks, chunks of 512 * {8, 16, 32} positions, longer than k, at least
+    it chunks, chunks of 4096, 8192 or 16384 positions, longer than k, at least
     two of them, and at most 32768 candidates for the final workgroup; rows of
     at most 4096 columns never chunk."""
     import _glm53_lib

@@ -152,7 +152,9 @@ def test_topk_ties_specials_and_short_rows(cuda, oracle):
 @pytest.mark.parametrize("n,k", [
     (4096, 512),      # one workgroup over the row, 4 keys per thread
     (32768, 16384),   # one workgroup over the row, 32 keys per thread (chunks would not exceed k)
-    (65536, 512),     # chunks of 4096, 8192 candidates (from 32 rows: chunks of 8192, 4096)
+    (16384, 512),     # 512-thread workgroups over chunks of 4096, 2048 candidates
+    (65536, 512),     # 1024-thread workgroups over chunks of 8192, 4096 candidates (from 32 rows:
+                      # 512-thread workgroups over the same chunks)
     (20000, 8192),    # chunks of 16384, 16384 candidates
     (140000, 4096),   # too many candidates: sweeps over the row
 ])
