@@ -18,7 +18,9 @@
 //     per SIMD interleave their tiles, hiding each other's latencies.
 //     Splits of exactly three tiles (65-96 keys: B=8's 23 splits) take a
 //     12-wave variant, 3 key groups x 4 slices, that consumes them in one
-//     round instead of two (the second with one group idle).
+//     round instead of two (the second with one group idle); one-tile
+//     splits (B=1's 68) a 4-wave variant, one key group, whose partials
+//     leave the accumulators with no LDS combine.
 //   * Lane (g = lane / 16, c = lane % 16) gathers 32 bytes of its wave's
 //     slice from keys c and 16 + c of a tile: four 16-byte loads per tile,
 //     slice bytes 16g + [0, 16) and 64 + 16g + [0, 16), so each load
@@ -71,7 +73,7 @@ struct MlaArgs {
   int num_splits;
   int split_len;
   float scale_log2;
-  float* part;    // [T][S][Hp][512] fp32 (num_splits > 1)
+  float* part;    // fp32 blocks of 16 heads x 512 per (t, split, head group), accumulator order (part_block)
   float* lse;     // [T][S][Hp]
   int heads_padded;
   uint16_t* out;
