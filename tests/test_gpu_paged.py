@@ -12,11 +12,9 @@ import torch
 
 import workloads as W
 from conftest import log_case
+from mla_bar import check_bar
 
 pytestmark = pytest.mark.gpu
-
-MAX_ABS = 2e-2
-MEAN_ABS = 2e-3
 
 
 def paged_cache(cuda, num_blocks, block_size, page_bytes, seed):
@@ -122,9 +120,7 @@ def test_paged_attention(cuda, oracle, splits, block_size, page_bytes):
         lc = pages_np[btn[reqn[t]]].reshape(-1, 528)
         li = np.where((idxn[t] >= 0) & (idxn[t] < lc.shape[0]), idxn[t], -1)[None, :]
         want = bf16_to_f32(oracle.sparse_mla(qn[t:t + 1], lc, li, W.SM_SCALE, n_splits=1))[0]
-        err = np.abs(got[t] - want)
-        ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(want), 2.0 ** -126))) - 7)
-        assert np.all(err <= np.maximum(MAX_ABS, ulp)) and err.mean() <= MEAN_ABS, (t, err.max())
+        check_bar(got[t], want, f"paged token {t}")
 
 
 def test_paged_random_shapes(cuda):
