@@ -383,6 +383,7 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_mqa_logits_rows_kernel(cons
 // ------------------------------------------------------------------ top-k
 constexpr int kHistBins = 4096;
 constexpr int kChunkThreads = 512;
+constexpr int kChunkThreadsWide = 1024;   // chunk workgroups of the few-rows plan (8 keys per thread)
 constexpr int kFinalThreads = 1024;
 constexpr int kSweepThreads = 1024;
 constexpr int kSweepKeys = 32;                      // keys per thread per sweep
@@ -952,9 +953,9 @@ TopkPlan plan_topk(int64_t num_rows, int64_t max_len, int64_t k) {
   if (max_len <= int64_t(kFinalThreads) * 4) return {TopkPlan::kDirect, 0, 4, 0, 0, 0};
   TopkPlan best{TopkPlan::kSweepMode, 0, 0, 0, 0, 0};
   int best_cost = 1 << 30;
-  for (int threads : {kChunkThreads, kFinalThreads}) {
+  for (int threads : {kChunkThreads, kChunkThreadsWide}) {
     for (int p : {8, 16, 32}) {
-      if (threads == kFinalThreads && p != 8) continue;
+      if (threads == kChunkThreadsWide && p != 8) continue;
       const int64_t len_c = int64_t(threads) * p;
       if (len_c <= k) continue;
       const int64_t chunks = (max_len + len_c - 1) / len_c;
@@ -1025,8 +1026,8 @@ extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t
   const bool cand = plan.mode == TopkPlan::kChunked;
   if (cand) {
     const dim3 grid(static_cast<unsigned>(num_rows), static_cast<unsigned>(plan.chunks));
-    if (plan.chunk_threads == kFinalThreads)
-      hipLaunchKernelGGL((topk_chunk_kernel<8, kFinalThreads>), grid, dim3(kFinalThreads), 0, st, a);
+    if (plan.chunk_threads == kChunkThreadsWide)
+      hipLaunchKernelGGL((topk_chunk_kernel<8, kChunkThreadsWide>), grid, dim3(kChunkThreadsWide), 0, st, a);
     else switch (plan.chunk_p) {
       case 8: hipLaunchKernelGGL((topk_chunk_kernel<8, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
       case 16: hipLaunchKernelGGL((topk_chunk_kernel<16, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
