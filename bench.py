@@ -50,7 +50,16 @@ def log(*a):
 
 
 class Timer:
-    """Events recorded on the current stream (the one the kernels use)."""
+    """Events recorded on the current stream (the one the kernels use).
+
+    One untimed replay of the same graph runs just before a timed region
+    (no synchronisation between them), so the GPU is busy while the host
+    queues the timed replays: the region then times k replays that follow
+    each other as the steps of a decode loop do, rather than also the
+    graph launch latency of its first replay, which a short run (k = 2
+    replays of a 10-step graph) would spread over its few steps (B=8 over
+    the rotation: 11.97 -> 11.90 us per step at k = 2, 11.72 at k = 20
+    either way)."""
 
     def __init__(self, torch):
         self.torch = torch
@@ -60,6 +69,7 @@ class Timer:
         torch.cuda.synchronize()
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
+        graph.replay()   # untimed lead replay
         s.record()
         for _ in range(k):
             graph.replay()
@@ -67,8 +77,28 @@ class Timer:
         torch.cuda.synchronize()
         return s.elapsed_time(e) * 1e3 / k          # us per replay
 
+    def warm_clocks(self, graph, min_ms: float = 20.0) -> None:
+        """Untimed replays for at least min_ms of GPU time: out of idle the
+        part runs its first milliseconds at lower clocks (B=8 over the
+        rotation, 2-replay samples: 12.17 us per step right after 0.5 s idle,
+        11.92 after 200 replays), and a decode loop runs at busy clocks."""
+        torch = self.torch
+        torch.cuda.synchronize()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record()
+        done = 0.0
+        while done < min_ms:
+            for _ in range(10):
+                graph.replay()
+            e.record()
+            torch.cuda.synchronize()
+            done = s.elapsed_time(e)
+
     def median_loop(self, graph, k: int, samples: int = 5) -> float:
-        """Median over `samples` timings of k replays (us per replay)."""
+        """Median over `samples` timings of k replays (us per replay), after
+        warm_clocks."""
+        self.warm_clocks(graph)
         return statistics.median(self.replay_loop(graph, k) for _ in range(samples))
 
     def cold_loop(self, graph, k: int, flush) -> float:
