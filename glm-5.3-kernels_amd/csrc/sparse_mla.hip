@@ -1337,7 +1337,8 @@ namespace {
 
 // Static device scratch of glm53_sparse_mla_noalloc: the split partials of
 // at most GLM53_NOALLOC_MAX_PARTIAL_ROWS (token, split, head) rows, laid out
-// as the workspace of glm53_sparse_mla (part [rows][512], then lse [rows]).
+// as the workspace of glm53_sparse_mla (rows x 512 floats of partials in
+// their accumulator-order blocks, then lse [rows]).
 // Every GPU the library runs on holds its own copy until the process ends.
 static __device__ __align__(256) float scratch[GLM53_NOALLOC_MAX_PARTIAL_ROWS * (kLatent + 1)];
 
