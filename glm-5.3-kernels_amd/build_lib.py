@@ -23,6 +23,11 @@ HIPCC_FLAGS = [
     "-ffp-contract=off",
     # keep MFMA accumulators in VGPRs (no AGPR copies around VALU rescales)
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # the leading 16 dwords of scalar kernel arguments arrive in SGPRs at
+    # wave launch instead of through the first scalar loads (kernels whose
+    # arguments are one struct keep loading them; code objects carry the
+    # fallback loads for firmware without preloading)
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
