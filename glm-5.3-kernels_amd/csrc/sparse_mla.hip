@@ -257,8 +257,15 @@ __device__ __forceinline__ uint16_t* vbuf_at(Shared& sh, int w, int row, int col
   return &sh.vbuf[w][row][(chunk << 3) | (col & 7)];
 }
 
+// The fields a split workgroup needs before its first loads come ahead of
+// MlaArgs as scalar arguments (the grid dims among them): the library is
+// built to preload the first 16 dwords of scalar arguments into SGPRs, so
+// these arrive with the wave instead of through a scalar load that would
+// head the index -> row chain.
 template <int kMode, bool kPipe, int kG>
-__global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(const MlaArgs a) {
+__global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
+    const int32_t* __restrict__ idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z,
+    int num_heads, const uint16_t* __restrict__ q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
   constexpr bool kPaged = kMode != kFlatRows;
   constexpr int kWaves = SplitShape<kG>::kWaves;
   constexpr int kChunkTiles = SplitShape<kG>::kChunkTiles;
@@ -274,12 +281,12 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
   // (Other unit counts keep the plain mapping: the divisions cost B=1
   // 0.35 us for nothing.)
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
-  if ((gridDim.y * gridDim.z) % 8 == 0) {
-    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int units = gridDim.y * gridDim.z;
+  if ((grid_y * grid_z) % 8 == 0) {
+    const int lin = blockIdx.x + grid_x * (blockIdx.y + grid_y * blockIdx.z);
+    const int units = grid_y * grid_z;
     split = lin / units;
-    t = (lin % units) % gridDim.y;
-    hg = (lin % units) / gridDim.y;
+    t = (lin % units) % grid_y;
+    hg = (lin % units) / grid_y;
   }
   const int w = uniform(threadIdx.x >> 6);
   const int sl = w & (kSlices - 1);
@@ -287,11 +294,11 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   const int c = lane & 15;
-  const int start = split * a.split_len;
-  const int end = min(start + a.split_len, a.topk);
+  const int start = split * split_len;
+  const int end = min(start + split_len, topk);
   const int head = hg * kHeads + c;
-  const bool head_ok = head < a.num_heads;
-  const int32_t* idx_t = a.idx + t * a.si_t;
+  const bool head_ok = head < num_heads;
+  const int32_t* idx_t = idx + t * si_t;
   // A request id outside the block table maps every index to -1.
   const int req = kPaged ? a.req_id[t] : 0;
   const bool req_ok = req >= 0 && req < a.num_reqs;
@@ -383,7 +390,7 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(co
   // wait for them.
   bf16x8 qf[4];
   {
-    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (head_ok ? head : 0) * a.sq_h +
+    const uint4* qp = reinterpret_cast<const uint4*>(q + t * sq_t + (head_ok ? head : 0) * sq_h +
                                                      kSlice * sl + 16 * g);
     const uint4 z = make_uint4(0, 0, 0, 0);
     const uint4 q0 = qp[0], q1 = qp[1], q2 = qp[8], q3 = qp[9];
@@ -939,15 +946,17 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
 // duration is the floor that the split kernel's conversions, products and
 // softmax add to.
 template <int kG>
-__global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_floor_kernel(const MlaArgs a) {
+__global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_floor_kernel(
+    const int32_t* __restrict__ idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z,
+    int num_heads, const uint16_t* __restrict__ q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
   constexpr int kRounds = SplitShape<kG>::kRounds;
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
-  if ((gridDim.y * gridDim.z) % 8 == 0) {
-    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int units = gridDim.y * gridDim.z;
+  if ((grid_y * grid_z) % 8 == 0) {
+    const int lin = blockIdx.x + grid_x * (blockIdx.y + grid_y * blockIdx.z);
+    const int units = grid_y * grid_z;
     split = lin / units;
-    t = (lin % units) % gridDim.y;
-    hg = (lin % units) / gridDim.y;
+    t = (lin % units) % grid_y;
+    hg = (lin % units) / grid_y;
   }
   const int w = uniform(threadIdx.x >> 6);
   const int sl = w & (kSlices - 1);
@@ -955,9 +964,9 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
   const int c = lane & 15;
-  const int start = split * a.split_len;
-  const int end = min(start + a.split_len, a.topk);
-  const int32_t* idx_t = a.idx + t * a.si_t;
+  const int start = split * split_len;
+  const int end = min(start + split_len, topk);
+  const int32_t* idx_t = idx + t * si_t;
   const int head = hg * kHeads + c;
   // The split kernel's load order: the split's indices, q, then per tile the
   // row scale and the rows, all in flight before any is used (decode splits
@@ -968,7 +977,7 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
     const int pos = start + (kG * r + kg) * kTile + (lane & 31);
     ids[r] = pos < end ? idx_t[pos] : -1;
   }
-  const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (head < a.num_heads ? head : 0) * a.sq_h +
+  const uint4* qp = reinterpret_cast<const uint4*>(q + t * sq_t + (head < num_heads ? head : 0) * sq_h +
                                                    kSlice * sl + 16 * g);
   const uint4 q0 = qp[0], q1 = qp[1], q2 = qp[8], q3 = qp[9];
   uint32_t sv[kRounds];
@@ -994,7 +1003,7 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
       kd[r][u][1] = kid >= 0 ? k1 : z;
     }
   }
-  uint32_t fold = head < a.num_heads ? q0.x ^ q1.y ^ q2.z ^ q3.w : 0u;   // folded last: no early wait
+  uint32_t fold = head < num_heads ? q0.x ^ q1.y ^ q2.z ^ q3.w : 0u;   // folded last: no early wait
 #pragma unroll
   for (int r = 0; r < kRounds; r++) {
     fold ^= sv[r];
@@ -1011,7 +1020,7 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
 #pragma unroll
   for (int dt = 0; dt < 8; dt++)
     if (dt * kG / 8 == kg) *reinterpret_cast<float4*>(pb + dt * 64 * 4) = make_float4(x, x, x, x);
-  if (head < a.num_heads && kg == 0 && sl == 0 && g == 0)
+  if (head < num_heads && kg == 0 && sl == 0 && g == 0)
     a.lse[(static_cast<int64_t>(t) * a.num_splits + split) * a.heads_padded + head] = x;
 }
 
@@ -1074,7 +1083,7 @@ constexpr int kMergeThreads = kMergeLanes * 64;
 __global__ __launch_bounds__(kMergeThreads) void sparse_mla_merge_kernel(const float* __restrict__ part,
                                                                           const float* __restrict__ lse,
                                                                           int num_splits, int heads_padded,
-                                                                          int num_heads,
+                                                                          int num_heads, int num_tokens,
                                                                           uint16_t* __restrict__ out,
                                                                           int64_t so_t, int64_t so_h) {
   __shared__ float red_m[kMergeLanes][64];
@@ -1082,11 +1091,12 @@ __global__ __launch_bounds__(kMergeThreads) void sparse_mla_merge_kernel(const f
   __shared__ __attribute__((aligned(16))) float4 part_sum[kMergeLanes][64];
   // token fastest in the linear id: with a multiple of 8 tokens, token t's
   // workgroups share the XCD that ran its splits
+  // (num_tokens * groups is gridDim.x, passed in with the leading arguments
+  // so that it arrives preloaded)
   const int groups = heads_padded / kHeads;
-  const int num_tokens = gridDim.x / groups;
   int t = blockIdx.x / groups, hg = blockIdx.x % groups, tile = blockIdx.y;
   if (num_tokens % 8 == 0) {
-    const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int lin = blockIdx.x + num_tokens * groups * blockIdx.y;
     t = lin % num_tokens;
     hg = (lin / num_tokens) % groups;
     tile = lin / (num_tokens * groups);
@@ -1239,7 +1249,9 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   // Splits longer than one chunk of gathers pipeline their chunks.
   const bool pipe = a.split_len > kChunkTiles * kTile;
   const int mode = a.pools != nullptr ? kPooledPos : a.bt != nullptr ? kPagedPos : kFlatRows;
-#define GLM53_LAUNCH(M, P) hipLaunchKernelGGL((sparse_mla_kernel<M, P, 2>), grid, dim3(kThreads), 0, st, a)
+#define GLM53_LEAD a.idx, a.si_t, a.split_len, a.topk, static_cast<int>(grid.x), static_cast<int>(grid.y), \
+                   static_cast<int>(grid.z), a.num_heads, a.q, a.sq_t, a.sq_h, a
+#define GLM53_LAUNCH(M, P) hipLaunchKernelGGL((sparse_mla_kernel<M, P, 2>), grid, dim3(kThreads), 0, st, GLM53_LEAD)
 #define GLM53_PAIR(M) hipLaunchKernelGGL((sparse_mla_pair_kernel<M>), grid, dim3(128), 0, st, a)
   // Long splits go to the pair kernel, whose masked keys read row 0 (page 0):
   // it needs a non-empty cache (seq_kv counts rows, or pages when paged).
@@ -1249,7 +1261,7 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   const bool three = a.split_len > 2 * kTile && a.split_len <= 3 * kTile;
   const bool one = a.split_len <= kTile;
 #define GLM53_KG(M, G) hipLaunchKernelGGL((sparse_mla_kernel<M, false, G>), grid, \
-                                          dim3(SplitShape<G>::kThreads), 0, st, a)
+                                          dim3(SplitShape<G>::kThreads), 0, st, GLM53_LEAD)
   if (mode == kPooledPos) {
     if (pair) GLM53_PAIR(kPooledPos); else if (pipe) GLM53_LAUNCH(kPooledPos, true);
     else if (three) GLM53_KG(kPooledPos, 3); else if (one) GLM53_KG(kPooledPos, 1); else GLM53_LAUNCH(kPooledPos, false);
@@ -1263,13 +1275,15 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
 #undef GLM53_KG
 #undef GLM53_PAIR
 #undef GLM53_LAUNCH
+#undef GLM53_LEAD
 }
 
 void launch_merge(const float* part, const float* lse, int64_t num_tokens, int num_splits,
                   int heads_padded, int num_heads, uint16_t* out, int64_t so_t, int64_t so_h,
                   hipStream_t st) {
   hipLaunchKernelGGL(sparse_mla_merge_kernel, dim3(static_cast<unsigned>(num_tokens * (heads_padded / kHeads)), 32),
-                     dim3(kMergeThreads), 0, st, part, lse, num_splits, heads_padded, num_heads, out, so_t, so_h);
+                     dim3(kMergeThreads), 0, st, part, lse, num_splits, heads_padded, num_heads,
+                     static_cast<int>(num_tokens), out, so_t, so_h);
 }
 
 }  // namespace
@@ -1572,14 +1586,16 @@ extern "C" int glm53_sparse_mla_gather_floor(const void* q, int64_t sq_t, int64_
   (void)hipGetLastError();
   // the split kernel's workgroup shape for this split length (three key
   // groups for 3-tile splits, one for 1-tile splits)
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+#define GLM53_LEAD a.idx, a.si_t, a.split_len, a.topk, static_cast<int>(grid.x), static_cast<int>(grid.y), \
+                   static_cast<int>(grid.z), a.num_heads, a.q, a.sq_t, a.sq_h, a
   if (a.split_len > 2 * kTile && a.split_len <= 3 * kTile)
-    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<3>, grid, dim3(SplitShape<3>::kThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<3>, grid, dim3(SplitShape<3>::kThreads), 0, st, GLM53_LEAD);
   else if (a.split_len <= kTile)
-    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<1>, grid, dim3(SplitShape<1>::kThreads), 0,
-                       static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<1>, grid, dim3(SplitShape<1>::kThreads), 0, st, GLM53_LEAD);
   else
-    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<2>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+    hipLaunchKernelGGL(sparse_mla_gather_floor_kernel<2>, grid, dim3(kThreads), 0, st, GLM53_LEAD);
+#undef GLM53_LEAD
   return static_cast<int>(hipGetLastError());
 }
 
