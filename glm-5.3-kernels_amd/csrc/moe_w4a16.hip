@@ -468,7 +468,9 @@ __device__ __forceinline__ void stream_finish(const GateUpArgs& a, const f32x4& 
 }
 
 template <bool kSelfAlign, int kTiles, int kKSplit>
-__global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_stream_kernel(const GateUpArgs a) {
+__global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_stream_kernel(
+    const void* topk_ids, int ids_i64, int num_routes, const uint4* w13, const uint16_t* s13, const uint16_t* x,
+    int64_t sx, int n_inter, int num_experts, const GateUpArgs a) {
   constexpr int kW = kTiles * kKSplit;             // waves
   constexpr int kCpw = kStreamChunks / kKSplit;    // chunks per wave
   constexpr int kXPer = kWaves / kW;               // 512-feature activation pieces staged per wave
@@ -477,17 +479,17 @@ __global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_strea
   __shared__ __attribute__((aligned(16))) uint16_t xsh[kBlock][kXStride];
   __shared__ f32x4 red[kKSplit > 1 ? kW : 1][2][64];
   const int b = blockIdx.x;
-  const int n_half = a.n_inter / kTileN;
+  const int n_half = n_inter / kTileN;
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   const int col = lane & 15;
-  const int R = a.num_routes;
+  const int R = num_routes;
 
   int slot[kBlock];   // route of each slot of the block (R = padding); wave-uniform
   int e;
   if (kSelfAlign) {
     const bool in = lane < R;
-    const RoutePos rp = align_routes(in ? load_route_id(a.topk_ids, a.ids_i64, lane) : -1, in);
+    const RoutePos rp = align_routes(in ? load_route_id(topk_ids, ids_i64, lane) : -1, in);
 #pragma unroll
     for (int m = 0; m < kBlock; m++) {
       const uint64_t hit = __ballot(rp.valid && rp.pos == kBlock * b + m);
@@ -499,7 +501,7 @@ __global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_strea
 #pragma unroll
     for (int m = 0; m < kBlock; m++) slot[m] = a.sorted_ids[kBlock * b + m];
   }
-  if (e < 0 || e >= a.num_experts) return;   // unused block (uniform over the workgroup)
+  if (e < 0 || e >= num_experts) return;   // unused block (uniform over the workgroup)
 
   // Activation rows: wave w stages features 512 (w + kW p) + [0, 512) of
   // every routed slot with direct global->LDS loads (no registers held while
@@ -510,7 +512,7 @@ __global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_strea
     if (slot[m] < R) {   // uniform
       const unsigned r = static_cast<unsigned>(slot[m]);
       const unsigned tok = a.topk_log2 >= 0 ? r >> a.topk_log2 : r / static_cast<unsigned>(a.topk);
-      const uint16_t* xr = a.x + static_cast<int64_t>(tok) * a.sx;
+      const uint16_t* xr = x + static_cast<int64_t>(tok) * sx;
 #pragma unroll
       for (int p = 0; p < kXPer; p++)
         __builtin_amdgcn_global_load_lds(xr + 512 * (w + kW * p) + 8 * lane, &xsh[m][512 * (w + kW * p)], 16, 0, 0);
@@ -523,10 +525,10 @@ __global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_strea
   const int64_t tg = (static_cast<int64_t>(e) * 2 * n_half + jtc) * kStreamChunks;
   const int64_t tu = tg + static_cast<int64_t>(n_half) * kStreamChunks;
   // uniform tile bases (SGPRs); each access adds the lane's 32-bit offset
-  const uint4* wg = a.w13 + tg * 64;
-  const uint4* wu = a.w13 + tu * 64;
-  const uint2* sg = reinterpret_cast<const uint2*>(a.s13 + tg * 64);
-  const uint2* su = reinterpret_cast<const uint2*>(a.s13 + tu * 64);
+  const uint4* wg = w13 + tg * 64;
+  const uint4* wu = w13 + tu * 64;
+  const uint2* sg = reinterpret_cast<const uint2*>(s13 + tg * 64);
+  const uint2* su = reinterpret_cast<const uint2*>(s13 + tu * 64);
   const int c0 = part * kCpw;
   StreamRing ring;
 #pragma unroll
@@ -602,32 +604,34 @@ struct __align__(16) DownShared {
   float part[kWaves][kTileN];
 };
 
-__global__ __launch_bounds__(kThreads) void moe_w4a16_down_kernel(const DownArgs a) {
+__global__ __launch_bounds__(kThreads) void moe_w4a16_down_kernel(
+    const void* topk_ids, int ids_i64, int topk, int64_t sid_t, const uint4* w2, const uint16_t* s2,
+    const uint16_t* act, int n_inter, int hidden, const DownArgs a) {
   __shared__ DownShared sh;
   const int nt = blockIdx.x;
   const int t = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   const int q = lane >> 4, col = lane & 15;
-  const int k_chunks = a.n_inter / kChunkK;
-  const int n_tiles2 = a.hidden / kTileN;
-  const bool has_route = w < a.topk;   // wave w computes route slot w (topk <= 8)
+  const int k_chunks = n_inter / kChunkK;
+  const int n_tiles2 = hidden / kTileN;
+  const bool has_route = w < topk;   // wave w computes route slot w (topk <= 8)
 
   // Route of this wave (the same id in every lane).
   int e = -1;
   if (has_route) {
-    const int64_t raw = load_route_id(a.topk_ids, a.ids_i64, static_cast<int>(t * a.sid_t + w));
+    const int64_t raw = load_route_id(topk_ids, ids_i64, static_cast<int>(t * sid_t + w));
     e = uniform(raw >= 0 && raw < a.num_experts ? static_cast<int>(raw) : -1);
   }
-  const uint4* wp = a.w2 + ((static_cast<int64_t>(e < 0 ? 0 : e) * n_tiles2 + nt) * k_chunks) * 64 + lane;
-  const uint16_t* sp = a.s2 + ((static_cast<int64_t>(e < 0 ? 0 : e) * n_tiles2 + nt) * k_chunks) * 64 + 4 * col;
+  const uint4* wp = w2 + ((static_cast<int64_t>(e < 0 ? 0 : e) * n_tiles2 + nt) * k_chunks) * 64 + lane;
+  const uint16_t* sp = s2 + ((static_cast<int64_t>(e < 0 ? 0 : e) * n_tiles2 + nt) * k_chunks) * 64 + 4 * col;
   // The wave's own c2 row into LDS with direct global->LDS loads (lane i ->
   // 16 bytes at i*16), then the first weight batch; only this wave reads the
   // row, so no workgroup barrier is needed before the MFMA loop.
-  const uint16_t* act_r = a.act + (static_cast<int64_t>(t) * a.topk + w) * a.n_inter;
+  const uint16_t* act_r = act + (static_cast<int64_t>(t) * topk + w) * n_inter;
   if (e >= 0) {
-    for (int k0 = 0; k0 < a.n_inter; k0 += 8 * 64)
-      if (k0 + 8 * lane < a.n_inter)
+    for (int k0 = 0; k0 < n_inter; k0 += 8 * 64)
+      if (k0 + 8 * lane < n_inter)
         __builtin_amdgcn_global_load_lds(act_r + k0 + 8 * lane, &sh.act[w][k0], 16, 0, 0);
   }
   uint4 kw[kBatch];
@@ -665,7 +669,7 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_down_kernel(const DownArgs
   __syncthreads();
   if (threadIdx.x < kTileN) {
     float s = 0.f;
-    for (int ww = 0; ww < a.topk; ww++) s += sh.part[ww][threadIdx.x];
+    for (int ww = 0; ww < topk; ww++) s += sh.part[ww][threadIdx.x];
     a.out[t * a.so + kTileN * nt + threadIdx.x] = static_cast<uint16_t>(f32_to_bf16_bits(s));
   }
 }
@@ -745,7 +749,11 @@ int launch_gate_up(bool self_align, const void* x, int64_t sx, const void* w13, 
     const int tiles = pairs >= 8 * num_cus() ? 8 : pairs >= 4 * num_cus() ? 4 : pairs >= 2 * num_cus() ? 2 : 1;
     const dim3 gs(static_cast<unsigned>(num_routes), static_cast<unsigned>((n_half + tiles - 1) / tiles));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    auto go = [&](auto kernel, int waves) { hipLaunchKernelGGL(kernel, gs, dim3(64 * waves), 0, st, a); };
+    // the fields the first loads need lead, as scalars (preloaded into SGPRs)
+    auto go = [&](auto kernel, int waves) {
+      hipLaunchKernelGGL(kernel, gs, dim3(64 * waves), 0, st, a.topk_ids, a.ids_i64, a.num_routes, a.w13, a.s13,
+                         a.x, a.sx, a.n_inter, a.num_experts, a);
+    };
     if (tiles == 8)
       self_align ? go(moe_w4a16_gate_up_stream_kernel<true, 8, 1>, 8) : go(moe_w4a16_gate_up_stream_kernel<false, 8, 1>, 8);
     else if (tiles == 4)
@@ -792,7 +800,8 @@ extern "C" int glm53_moe_w4a16_down(const void* act, const void* w2, const void*
              static_cast<uint16_t*>(out), so};
   (void)hipGetLastError();
   hipLaunchKernelGGL(moe_w4a16_down_kernel, dim3(static_cast<unsigned>(hidden / kTileN), static_cast<unsigned>(num_tokens)),
-                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+                     dim3(kThreads), 0, static_cast<hipStream_t>(stream), a.topk_ids, a.ids_i64, a.topk, a.sid_t,
+                     a.w2, a.s2, a.act, a.n_inter, a.hidden, a);
   return static_cast<int>(hipGetLastError());
 }
 
