@@ -180,25 +180,27 @@ __device__ __forceinline__ void load_group(const LogitsArgs& a, int t, int j0, i
 // for stores after the last load (stores count with the loads in vmcnt):
 // every wait then counts exactly the group it needs.
 template <int kTiles, int kN, bool kAligned>
-__global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(const LogitsArgs a) {
+__global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(
+    const int32_t* ctx, const int32_t* bt, int64_t bt_stride, const uint8_t* q, int64_t sq_t, int keys_per_wg,
+    int max_len, int block_size, int max_blocks, const LogitsArgs a) {
   constexpr int kDepth = 4;
   const int t = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int w = uniform(threadIdx.x >> 6);
   const int g = lane >> 4, c = lane & 15;
-  const int j_wave = blockIdx.x * a.keys_per_wg + w * 16 * kN;
-  const int j_end = j_wave + 16 * kN < a.max_len ? j_wave + 16 * kN : a.max_len;
+  const int j_wave = blockIdx.x * keys_per_wg + w * 16 * kN;
+  const int j_end = j_wave + 16 * kN < max_len ? j_wave + 16 * kN : max_len;
   if (j_wave >= j_end) return;   // uniform (no barriers in this kernel)
   const int n = (j_end - j_wave + 15) / 16;
-  const int cap = a.max_blocks * a.block_size;
-  int len = a.ctx[t];
+  const int cap = max_blocks * block_size;
+  int len = ctx[t];
   len = len < 0 ? 0 : len > cap ? cap : len;
 
   // page of each group's first key (lane i < n: group i; -1 past the context)
   int blk_l = -1;
   if (lane < n) {
     const int j0 = j_wave + 16 * lane;
-    if (j0 < len) blk_l = a.bt[t * a.bt_stride + j0 / a.block_size];
+    if (j0 < len) blk_l = bt[t * bt_stride + j0 / block_size];
   }
 
   // q fragments (A operand) and the weights of this lane's heads.
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(con
   float wv[kTiles][4];
 #pragma unroll
   for (int ht = 0; ht < kTiles; ht++) {
-    const uint4* qp = reinterpret_cast<const uint4*>(a.q + t * a.sq_t + (16 * ht + c) * a.sq_h + 16 * g);
+    const uint4* qp = reinterpret_cast<const uint4*>(q + t * sq_t + (16 * ht + c) * a.sq_h + 16 * g);
     const uint4 lo = qp[0], hi = qp[4];
     qf[ht][0] = (static_cast<uint64_t>(lo.y) << 32) | lo.x;
     qf[ht][1] = (static_cast<uint64_t>(lo.w) << 32) | lo.z;
@@ -660,31 +662,35 @@ __device__ __forceinline__ void for_each_key(const uint32_t (&kk)[P], F&& f) {
   for (int j = 0; j < P; j++) f(kk[j]);
 }
 
-__device__ __forceinline__ int clamp_len(const TopkArgs& a, int row) {
-  const int len = a.lengths[row];
-  return len < 0 ? 0 : len > a.max_len ? a.max_len : len;
+__device__ __forceinline__ int clamp_len(const int32_t* lengths, int max_len, int row) {
+  const int len = lengths[row];
+  return len < 0 ? 0 : len > max_len ? max_len : len;
 }
+
+__device__ __forceinline__ int clamp_len(const TopkArgs& a, int row) { return clamp_len(a.lengths, a.max_len, row); }
 
 // Chunk stage: workgroup (row, chunk c) keeps the local top-k of positions
 // [c * chunk_len, (c + 1) * chunk_len) of the row, in position order, as
 // candidates (every valid position when the chunk holds at most k).  A key of
 // the row's top k is in its chunk's top k, so the candidates hold the answer.
 template <int P, int kThreads>
-__global__ __launch_bounds__(kThreads) void topk_chunk_kernel(const TopkArgs a) {
+__global__ __launch_bounds__(kThreads) void topk_chunk_kernel(
+    const float* p_logits, int64_t p_sl, const int32_t* p_lengths, int p_max_len, int p_k, int p_chunk_len,
+    int p_chunks, int p_vec, const TopkArgs a) {
   __shared__ SelShared<kThreads> sh;
   const int row = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
-  const int len = clamp_len(a, row);
-  const int k = a.k;
-  const int start = c * a.chunk_len;
+  const int len = clamp_len(p_lengths, p_max_len, row);
+  const int k = p_k;
+  const int start = c * p_chunk_len;
   const int rest = len - start;
-  const int valid = rest < 0 ? 0 : rest > a.chunk_len ? a.chunk_len : rest;
+  const int valid = rest < 0 ? 0 : rest > p_chunk_len ? p_chunk_len : rest;
   if (len <= k || valid == 0) return;   // uniform
   float f[P];
-  issue_row_loads<P>(a.logits + row * a.sl + start, valid, tid * P, a.vec, f);
+  issue_row_loads<P>(p_logits + row * p_sl + start, valid, tid * P, p_vec, f);
   if (valid > k) clear_hist(sh);   // under the loads' latency (uniform)
   uint32_t kk[P];
   form_keys<P>(f, valid, tid * P, kk);
-  const int64_t cb = (static_cast<int64_t>(row) * a.chunks + c) * k;
+  const int64_t cb = (static_cast<int64_t>(row) * p_chunks + c) * k;
   uint32_t* ck = a.cand_key + cb;
   int32_t* cp = a.cand_pos + cb;
   if (valid <= k) {
@@ -714,12 +720,14 @@ __global__ __launch_bounds__(kThreads) void topk_chunk_kernel(const TopkArgs a) 
 // valid positions can be short and every empty slot (key 0) follows every
 // filled one: never selected.
 template <int P, bool kCand>
-__global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(const TopkArgs a) {
+__global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(
+    const int32_t* p_lengths, int p_max_len, int p_k, int p_chunks, uint32_t* p_cand_key, int32_t* p_cand_pos,
+    int32_t* p_out, int64_t p_so, int p_chunk_len, const TopkArgs a) {
   __shared__ SelShared<kFinalThreads> sh;
   const int row = blockIdx.x, tid = threadIdx.x;
-  const int len = clamp_len(a, row);
-  const int k = a.k;
-  int32_t* out = a.out + row * a.so;
+  const int len = clamp_len(p_lengths, p_max_len, row);
+  const int k = p_k;
+  int32_t* out = p_out + row * p_so;
   if (len <= k) {   // every valid position is selected (uniform)
     for (int i = tid; i < k; i += kFinalThreads) out[i] = i < len ? i : -1;
     return;
@@ -727,41 +735,41 @@ __global__ __launch_bounds__(kFinalThreads) void topk_final_kernel(const TopkArg
   uint32_t kk[P];
   int32_t pos[kCand ? P : 1];
   uint32_t kmin = ~0u, kmax = 0u;
-  const int64_t cb = kCand ? static_cast<int64_t>(row) * a.chunks * k : 0;
+  const int64_t cb = kCand ? static_cast<int64_t>(row) * p_chunks * k : 0;
   if (kCand) {
     // Candidate i = tid * P + j is slot sl of chunk c (i = c * k + sl).  The
     // loads are unconditional (issued together), from clamped indices when
     // k is not a multiple of 4, else as 4-candidate vectors (a vector never
     // straddles chunks then); filled slots are picked afterwards.
-    const int n_cand = a.chunks * k;
+    const int n_cand = p_chunks * k;
     if ((k & 3) == 0) {   // keys first: the first pass waits for them only
 #pragma unroll
       for (int q = 0; q < P / 4; q++) {
         const int i = tid * P + 4 * q < n_cand ? tid * P + 4 * q : n_cand - 4;
-        const uint4 kv = *reinterpret_cast<const uint4*>(a.cand_key + cb + i);
+        const uint4 kv = *reinterpret_cast<const uint4*>(p_cand_key + cb + i);
         kk[4 * q] = kv.x; kk[4 * q + 1] = kv.y; kk[4 * q + 2] = kv.z; kk[4 * q + 3] = kv.w;
       }
 #pragma unroll
       for (int q = 0; q < P / 4; q++) {
         const int i = tid * P + 4 * q < n_cand ? tid * P + 4 * q : n_cand - 4;
-        const int4 pv = *reinterpret_cast<const int4*>(a.cand_pos + cb + i);
+        const int4 pv = *reinterpret_cast<const int4*>(p_cand_pos + cb + i);
         pos[4 * q] = pv.x; pos[4 * q + 1] = pv.y; pos[4 * q + 2] = pv.z; pos[4 * q + 3] = pv.w;
       }
     } else {
 #pragma unroll
       for (int j = 0; j < P; j++) {
         const int i = tid * P + j < n_cand ? tid * P + j : n_cand - 1;
-        kk[j] = a.cand_key[cb + i];
-        pos[j] = a.cand_pos[cb + i];
+        kk[j] = p_cand_key[cb + i];
+        pos[j] = p_cand_pos[cb + i];
       }
     }
     clear_hist(sh);   // under the loads' latency
     int c = (tid * P) / k, sl = tid * P - c * k;
 #pragma unroll
     for (int j = 0; j < P; j++) {
-      const int rest = len - c * a.chunk_len;
+      const int rest = len - c * p_chunk_len;
       const int n_c = rest < 0 ? 0 : rest > k ? k : rest;
-      const bool ok = c < a.chunks && sl < n_c;
+      const bool ok = c < p_chunks && sl < n_c;
       kk[j] = ok ? kk[j] : 0u;
       if (ok) { kmin = min(kmin, kk[j]); kmax = max(kmax, kk[j]); }
       if (++sl == k) { sl = 0; c++; }
@@ -822,8 +830,13 @@ __global__ __launch_bounds__(kSweepThreads) void topk_sweep_kernel(const TopkArg
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
+// The per-token logits kernel: the fields of its first loads lead as scalar
+// arguments (preloaded into SGPRs), the rest in LogitsArgs.
+using LogitsKernel = void (*)(const int32_t*, const int32_t*, int64_t, const uint8_t*, int64_t, int, int, int, int,
+                              LogitsArgs);
+
 template <int kTiles, bool kAligned>
-void (*pick_logits_n(int gpw))(LogitsArgs) {
+LogitsKernel pick_logits_n(int gpw) {
   switch (gpw) {
     case 1: return fp8_paged_mqa_logits_kernel<kTiles, 1, kAligned>;
     case 2: return fp8_paged_mqa_logits_kernel<kTiles, 2, kAligned>;
@@ -836,7 +849,7 @@ void (*pick_logits_n(int gpw))(LogitsArgs) {
 // Kernel for 16 * tiles heads and gpw groups per wave (unaligned block
 // sizes: one group per wave only).
 template <bool kAligned>
-void (*pick_logits_kernel(int tiles, int gpw))(LogitsArgs) {
+LogitsKernel pick_logits_kernel(int tiles, int gpw) {
   if constexpr (kAligned) {
     switch (tiles) {
       case 1: return pick_logits_n<1, true>(gpw);
@@ -915,8 +928,9 @@ extern "C" int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t s
   const dim3 grid(static_cast<unsigned>((max_len + keys_per_wg - 1) / keys_per_wg), static_cast<unsigned>(num_tokens));
   (void)hipGetLastError();
   const int tiles = static_cast<int>(num_heads / 16);
-  void (*kernel)(LogitsArgs) = al ? pick_logits_kernel<true>(tiles, gpw) : pick_logits_kernel<false>(tiles, 1);
-  hipLaunchKernelGGL(kernel, grid, dim3(kLogitThreads), 0, static_cast<hipStream_t>(stream), a);
+  LogitsKernel kernel = al ? pick_logits_kernel<true>(tiles, gpw) : pick_logits_kernel<false>(tiles, 1);
+  hipLaunchKernelGGL(kernel, grid, dim3(kLogitThreads), 0, static_cast<hipStream_t>(stream), a.ctx, a.bt,
+                     a.bt_stride, a.q, a.sq_t, a.keys_per_wg, a.max_len, a.block_size, a.max_blocks, a);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -989,8 +1003,11 @@ bool topk_shape_ok(int64_t num_rows, int64_t max_len, int64_t k) {
 
 template <int P>
 void launch_final(bool cand, dim3 grid, hipStream_t st, const TopkArgs& a) {
-  void (*kernel)(TopkArgs) = cand ? topk_final_kernel<P, true> : topk_final_kernel<P, false>;
-  hipLaunchKernelGGL(kernel, grid, dim3(kFinalThreads), 0, st, a);
+  // the fields of the first loads lead as scalar arguments (preloaded into SGPRs)
+  void (*kernel)(const int32_t*, int, int, int, uint32_t*, int32_t*, int32_t*, int64_t, int, TopkArgs) =
+      cand ? topk_final_kernel<P, true> : topk_final_kernel<P, false>;
+  hipLaunchKernelGGL(kernel, grid, dim3(kFinalThreads), 0, st, a.lengths, a.max_len, a.k, a.chunks, a.cand_key,
+                     a.cand_pos, a.out, a.so, a.chunk_len, a);
 }
 
 }  // namespace
@@ -1026,13 +1043,23 @@ extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t
   const bool cand = plan.mode == TopkPlan::kChunked;
   if (cand) {
     const dim3 grid(static_cast<unsigned>(num_rows), static_cast<unsigned>(plan.chunks));
+    // the fields of the first loads lead as scalar arguments (preloaded into SGPRs)
+#define CHUNK_LEAD a.logits, a.sl, a.lengths, a.max_len, a.k, a.chunk_len, a.chunks, a.vec ? 1 : 0, a
     if (plan.chunk_threads == kChunkThreadsWide)
-      hipLaunchKernelGGL((topk_chunk_kernel<8, kChunkThreadsWide>), grid, dim3(kChunkThreadsWide), 0, st, a);
+      hipLaunchKernelGGL((topk_chunk_kernel<8, kChunkThreadsWide>), grid, dim3(kChunkThreadsWide), 0, st,
+                         CHUNK_LEAD);
     else switch (plan.chunk_p) {
-      case 8: hipLaunchKernelGGL((topk_chunk_kernel<8, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
-      case 16: hipLaunchKernelGGL((topk_chunk_kernel<16, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
-      default: hipLaunchKernelGGL((topk_chunk_kernel<32, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, a); break;
+      case 8:
+        hipLaunchKernelGGL((topk_chunk_kernel<8, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, CHUNK_LEAD);
+        break;
+      case 16:
+        hipLaunchKernelGGL((topk_chunk_kernel<16, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, CHUNK_LEAD);
+        break;
+      default:
+        hipLaunchKernelGGL((topk_chunk_kernel<32, kChunkThreads>), grid, dim3(kChunkThreads), 0, st, CHUNK_LEAD);
+        break;
     }
+#undef CHUNK_LEAD
   }
   switch (plan.final_p) {
     case 4: launch_final<4>(cand, rows_grid, st, a); break;
