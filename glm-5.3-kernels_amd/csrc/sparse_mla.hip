@@ -264,8 +264,8 @@ __device__ __forceinline__ uint16_t* vbuf_at(Shared& sh, int w, int row, int col
 // head the index -> row chain.
 template <int kMode, bool kPipe, int kG>
 __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
-    const int32_t* __restrict__ idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z,
-    int num_heads, const uint16_t* __restrict__ q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
+    const int32_t* idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z, int num_heads,
+    const uint16_t* q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
   constexpr bool kPaged = kMode != kFlatRows;
   constexpr int kWaves = SplitShape<kG>::kWaves;
   constexpr int kChunkTiles = SplitShape<kG>::kChunkTiles;
@@ -947,8 +947,8 @@ void sparse_mla_pair_kernel(const MlaArgs a) {
 // softmax add to.
 template <int kG>
 __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_floor_kernel(
-    const int32_t* __restrict__ idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z,
-    int num_heads, const uint16_t* __restrict__ q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
+    const int32_t* idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z, int num_heads,
+    const uint16_t* q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
   constexpr int kRounds = SplitShape<kG>::kRounds;
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
   if ((grid_y * grid_z) % 8 == 0) {
