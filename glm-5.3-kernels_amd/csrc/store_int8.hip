@@ -73,12 +73,13 @@ __device__ __forceinline__ int64_t load_slot(const void* slots, int slots_i64, i
 // Fast path: x rows 16-byte aligned, destination rows 16-byte aligned.
 // ROWS rows per wave are loaded before any is reduced, so each lane keeps
 // ROWS independent 16-byte loads in flight.
+// The arguments of the first loads (latents, slots) lead: the library is
+// built to preload the leading 14 dwords of kernel arguments into SGPRs.
 template <int ROWS>
 __global__ __launch_bounds__(256) void store_int8_vec(const uint16_t* __restrict__ x, int64_t xs,
-                                                      uint8_t* __restrict__ cache, int64_t cs0,
-                                                      int64_t cs1, int64_t block, int64_t capacity,
-                                                      const void* __restrict__ slots,
-                                                      int slots_i64, int64_t n) {
+                                                      const void* __restrict__ slots, int64_t n,
+                                                      int slots_i64, uint8_t* __restrict__ cache, int64_t cs0,
+                                                      int64_t cs1, int64_t block, int64_t capacity) {
   const int wave = uniform(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave) * ROWS;
@@ -189,8 +190,8 @@ extern "C" int glm53_store_int8(const void* x, int64_t x_row_stride, void* cache
     const int64_t grid = (n_slots + rows_per_block - 1) / rows_per_block;
     if (grid > 0x7fffffff) return GLM53_ERR_BAD_SHAPE;
     hipLaunchKernelGGL(store_int8_vec<kRows>, dim3(static_cast<unsigned>(grid)), dim3(256), 0, st,
-                       xp, x_row_stride, cp, cache_stride_block, cache_stride_slot, block_size,
-                       capacity, slots, slots_is_i64, n_slots);
+                       xp, x_row_stride, slots, n_slots, slots_is_i64, cp, cache_stride_block,
+                       cache_stride_slot, block_size, capacity);
   } else {
     const int64_t grid = (n_slots + kWavesPerBlock - 1) / kWavesPerBlock;
     if (grid > 0x7fffffff) return GLM53_ERR_BAD_SHAPE;
