@@ -276,12 +276,14 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
 
   // Workgroups go to the 8 XCDs round robin by linear id; numbering the
   // (token, head group) units fastest puts all splits of a unit on one XCD
-  // when there are a multiple of 8 units (B=8: token t on XCD t), where the
-  // merge kernel reads them back.
-  // (Other unit counts keep the plain mapping: the divisions cost B=1
-  // 0.35 us for nothing.)
+  // when there are a multiple of 8 units (B=8: token t on XCD t), and on
+  // two XCDs for a multiple of 4 (B=4: token t on XCDs t and t + 4; 10.83
+  // -> 10.37 us per call over rotating caches), where the merge kernel
+  // reads them back.
+  // (Other unit counts keep the plain mapping: at B=1 the divisions cost
+  // 0.35 us for nothing, and B=2 gains nothing from four XCDs per token.)
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
-  if ((grid_y * grid_z) % 8 == 0) {
+  if ((grid_y * grid_z) % 4 == 0) {
     const int lin = blockIdx.x + grid_x * (blockIdx.y + grid_y * blockIdx.z);
     const int units = grid_y * grid_z;
     split = lin / units;
@@ -951,7 +953,7 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_gather_fl
     const uint16_t* q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
   constexpr int kRounds = SplitShape<kG>::kRounds;
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
-  if ((grid_y * grid_z) % 8 == 0) {
+  if ((grid_y * grid_z) % 4 == 0) {
     const int lin = blockIdx.x + grid_x * (blockIdx.y + grid_y * blockIdx.z);
     const int units = grid_y * grid_z;
     split = lin / units;
@@ -1089,13 +1091,13 @@ __global__ __launch_bounds__(kMergeThreads) void sparse_mla_merge_kernel(const f
   __shared__ float red_m[kMergeLanes][64];
   __shared__ float part_den[kMergeLanes][64];
   __shared__ __attribute__((aligned(16))) float4 part_sum[kMergeLanes][64];
-  // token fastest in the linear id: with a multiple of 8 tokens, token t's
-  // workgroups share the XCD that ran its splits
+  // token fastest in the linear id: with a multiple of 8 (4) tokens, token
+  // t's workgroups share the XCD (the two XCDs) that ran its splits
   // (num_tokens * groups is gridDim.x, passed in with the leading arguments
   // so that it arrives preloaded)
   const int groups = heads_padded / kHeads;
   int t = blockIdx.x / groups, hg = blockIdx.x % groups, tile = blockIdx.y;
-  if (num_tokens % 8 == 0) {
+  if (num_tokens % 4 == 0) {
     const int lin = blockIdx.x + num_tokens * groups * blockIdx.y;
     t = lin % num_tokens;
     hg = (lin / num_tokens) % groups;
