@@ -460,6 +460,22 @@ def main():
             timer.median_loop(fg1, max(1, K // args.unroll)) / args.unroll, 3)
         del grr, rot1, fg1
 
+        # ------------------------------------------------------------ B=4 layer rotation
+        # The first four query tokens of the B=8 workload over the same
+        # rotation (four units: each token's splits on two XCDs).
+        q4, idx4 = q8[:4].contiguous(), idx8[:4].contiguous()
+        gr4, _ = capture(torch, lambda: [triton_mla_sparse_attention(q4, rot[i % len(rot)], idx4, W.SM_SCALE,
+                                                                     num_kv_splits=args.splits)
+                                         for i in range(args.unroll)], 1)
+        for _ in range(3):
+            gr4.replay()
+        log("decode_b4 layer rotation")
+        us4 = timer.median_loop(gr4, max(1, K // args.unroll)) / args.unroll
+        extra["decode_b4"] = {"us_per_step_layer_rotation": round(us4, 3),
+                              "gbs_layer_rotation": round(W.mla_bytes(idx4, n_rows) / (us4 * 1e-6) / 1e9, 1),
+                              "workload": "tokens 0-3 of the B=8 decode workload"}
+        del gr4, q4, idx4
+
         # ------------------------------------------------------------ paged decode B=8
         # Request-relative indices: vLLM-style conversion + attention (two
         # launches before the attention's own) against the fused call.
