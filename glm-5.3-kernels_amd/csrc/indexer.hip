@@ -236,7 +236,6 @@ __global__ __launch_bounds__(kLogitThreads) void fp8_paged_mqa_logits_kernel(
       if (i + kDepth - 1 < kN) load(i + kDepth - 1, ring[(i + kDepth - 1) % kDepth]);
       if (i >= n) continue;   // uniform (the tail of a row)
       const Group& gr = ring[i % kDepth];
-      const int j = j_wave + 16 * i + c;
       float v = 0.f;
       if (gr.live) {
         const uint64_t k0 = (static_cast<uint64_t>(gr.kd[0].y) << 32) | gr.kd[0].x;
@@ -1012,9 +1011,16 @@ void launch_final(bool cand, dim3 grid, hipStream_t st, const TopkArgs& a) {
 
 }  // namespace
 
+// Enough for every call of at most num_rows rows: the plan switches to
+// 512-thread chunks at kTopkThroughputRows rows, whose candidates can take
+// less room than the latency plan's at fewer rows, so the query covers the
+// largest row count under that switch too.
 extern "C" int64_t glm53_indexer_topk_workspace_bytes(int64_t num_rows, int64_t max_len, int64_t k) {
   if (!topk_shape_ok(num_rows, max_len, k)) return 0;
-  return topk_ws_bytes(plan_topk(num_rows, max_len, k), num_rows, k);
+  const int64_t at_rows = topk_ws_bytes(plan_topk(num_rows, max_len, k), num_rows, k);
+  const int64_t below = num_rows < kTopkThroughputRows ? num_rows : kTopkThroughputRows - 1;
+  const int64_t at_below = topk_ws_bytes(plan_topk(below, max_len, k), below, k);
+  return at_rows > at_below ? at_rows : at_below;
 }
 
 extern "C" int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t* lengths, int64_t num_rows,

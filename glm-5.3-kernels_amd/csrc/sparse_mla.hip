@@ -54,9 +54,9 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kSlice = kLatent / kSlices;
 constexpr int kVStride = kSlice + 16;  // bf16 per LDS row: 288 bytes, rows 8 banks apart
 constexpr int kChunkTiles = 8;         // tiles whose gathers are in flight together
-constexpr int kRounds = kChunkTiles / kGroups;
 constexpr int kMergeLanes = 8;         // split lanes per output chunk in the LSE merge
 constexpr int kMaxMergeSplits = 1024;
+constexpr int kMaxGridTokens = 65535;   // query tokens per call: the split kernel's grid y
 constexpr float kNegLarge = -1.0e30f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -267,7 +267,6 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
     const int32_t* idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z, int num_heads,
     const uint16_t* q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
   constexpr bool kPaged = kMode != kFlatRows;
-  constexpr int kWaves = SplitShape<kG>::kWaves;
   constexpr int kChunkTiles = SplitShape<kG>::kChunkTiles;
   constexpr int kRounds = SplitShape<kG>::kRounds;
   constexpr int kRedBufs = SplitShape<kG>::kRedBufs;
@@ -1202,7 +1201,8 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
     return GLM53_ERR_BAD_SHAPE;
   if (num_tokens > 0 && (!q || (!kv && seq_kv > 0) || (!indices && topk > 0)))
     return GLM53_ERR_NULL_POINTER;
-  if (topk > 0x7fffffff || num_tokens > 0x7fffffff || num_splits > kMaxMergeSplits ||
+  // tokens are the grid's y dimension and head groups its z dimension
+  if (topk > 0x7fffffff || num_tokens > kMaxGridTokens || num_splits > kMaxMergeSplits ||
       (num_heads + kHeads - 1) / kHeads > 65535)
     return GLM53_ERR_BAD_SHAPE;
   if (reinterpret_cast<uintptr_t>(q) % 16 || sq_t % 8 || sq_h % 8 ||

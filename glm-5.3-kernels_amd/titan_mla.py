@@ -34,6 +34,9 @@ _MIN_BLOCK_N = 32
 KV_SPLITS_CANDIDATES = (1, 2, 4, 8, 16)
 _MIN_TOPK_PER_SPLIT = 128
 _SPLIT_MAX_OCCUPANCY = 4
+# Query tokens per library call (the split kernel's grid y); larger calls are
+# cut into consecutive token ranges.
+_MAX_TOKENS_PER_CALL = 65535
 
 
 def num_compute_units(device_index):
@@ -84,7 +87,7 @@ def _choose_num_kv_splits_mi355x(num_tokens: int, num_head_groups: int, index_to
     unchanged, for callers that want its exact answers.)
     """
     base = num_tokens * num_head_groups
-    if base == 0 or index_topk % _MIN_BLOCK_N:
+    if base == 0 or index_topk <= 0 or index_topk % _MIN_BLOCK_N:
         return 1
     tiles = index_topk // _MIN_BLOCK_N
     min_tiles = 1 if base == 1 else 2
@@ -142,6 +145,11 @@ def triton_mla_sparse_attention(
 
     out = torch.empty((num_tokens, num_heads_q, _BLOCK_DV), dtype=torch.bfloat16, device=q.device)
     if num_tokens == 0:
+        return out
+    if num_tokens > _MAX_TOKENS_PER_CALL:
+        for t0 in range(0, num_tokens, _MAX_TOKENS_PER_CALL):
+            t1 = min(t0 + _MAX_TOKENS_PER_CALL, num_tokens)
+            out[t0:t1] = triton_mla_sparse_attention(q[t0:t1], kv, indices[t0:t1], sm_scale, num_kv_splits)
         return out
 
     if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
@@ -222,6 +230,13 @@ def triton_mla_sparse_attention_paged(
     out = torch.empty((num_tokens, num_heads_q, _BLOCK_DV), dtype=torch.bfloat16, device=q.device)
     if num_tokens == 0:
         return out
+    if num_tokens > _MAX_TOKENS_PER_CALL:
+        for t0 in range(0, num_tokens, _MAX_TOKENS_PER_CALL):
+            t1 = min(t0 + _MAX_TOKENS_PER_CALL, num_tokens)
+            out[t0:t1] = triton_mla_sparse_attention_paged(q[t0:t1], kv_cache, req_indices[t0:t1],
+                                                           req_id_per_token[t0:t1], block_table, sm_scale,
+                                                           num_kv_splits)
+        return out
     if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
         q = q.contiguous()
     if req_indices.stride(1) != 1:
@@ -299,6 +314,13 @@ def triton_mla_sparse_attention_pooled(
         raise ValueError(f"num_kv_splits must be >= 1, got {num_kv_splits}")
     out = torch.empty((num_tokens, num_heads_q, _BLOCK_DV), dtype=torch.bfloat16, device=q.device)
     if num_tokens == 0:
+        return out
+    if num_tokens > _MAX_TOKENS_PER_CALL:
+        for t0 in range(0, num_tokens, _MAX_TOKENS_PER_CALL):
+            t1 = min(t0 + _MAX_TOKENS_PER_CALL, num_tokens)
+            out[t0:t1] = triton_mla_sparse_attention_pooled(
+                q[t0:t1], kv_cache, pool_ids[t0:t1], seq_lens[t0:t1] if seq_lens is not None else None,
+                pool_size, req_id_per_token[t0:t1], block_table, sm_scale, topk, num_kv_splits)
         return out
     if q.stride(2) != 1 or q.stride(1) % 8 or q.stride(0) % 8 or q.data_ptr() % 16:
         q = q.contiguous()

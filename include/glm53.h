@@ -62,7 +62,9 @@ int glm53_store_int8(const void* x, int64_t x_row_stride,
  * _sparse_mla_kernel_split and _sparse_mla_merge_kernel).
  *
  *   q        bf16 [num_tokens, num_heads, 512], strides sq_t, sq_h (elements),
- *            last dim contiguous, 16-byte aligned rows.
+ *            last dim contiguous, 16-byte aligned rows; num_tokens at most
+ *            65535 (the grid's y dimension) in this and every other
+ *            attention entry point, else GLM53_ERR_BAD_SHAPE.
  *   kv       528-byte rows, row r at kv + r * skv_t bytes (skv_t % 16 == 0),
  *            seq_kv rows; only the first 528 bytes of a row are read.
  *   indices  int32 [num_tokens, topk] with row stride si_t (elements); an
@@ -377,7 +379,9 @@ int glm53_fp8_paged_mqa_logits(const void* q, int64_t sq_t, int64_t sq_h,
  *   logits     fp32 [num_rows][max_len], row stride sl (rows 16-byte aligned load
  *              4 keys at a time, others one at a time)
  *   workspace  device scratch of glm53_indexer_topk_workspace_bytes(...) bytes
- *              (0 for rows of at most 4096 columns; may then be NULL)
+ *              (0 for rows of at most 4096 columns; may then be NULL); the
+ *              size asked for num_rows rows serves every call with at most
+ *              that many rows (same max_len and k)
  *   out        int32 [num_rows][k], row stride so
  */
 int64_t glm53_indexer_topk_workspace_bytes(int64_t num_rows, int64_t max_len,

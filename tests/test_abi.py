@@ -126,6 +126,7 @@ def test_library_split_policy_table():
         (1, 1, 2176, 70): 68,             # 68 <= 70
         (3, 1, 2176, 70): 23,             # cap 23 -> 3 tiles per split -> 23
         (0, 1, 2176, 256): 1,
+        (1, 1, 0, 256): 1, (8, 1, 0, 256): 1,   # no indices: one (empty) split
     }
     assert {k: pick(*k) for k in table} == table
 
@@ -390,3 +391,41 @@ def test_topk_plans_keep_their_invariants():
                 if chunk > k and chunks >= 2 and chunks * k <= 32768 and ws(3, max_len, k) == -(-(3 * chunks * k * 8) // 256) * 256:
                     ok = True
             assert ok, (max_len, k, per_row)
+
+
+def test_topk_workspace_query_covers_fewer_rows():
+    """glm53_indexer_topk_workspace_bytes(n, ...) is enough for every call of
+    at most n rows: the plan moves to 512-thread chunks at 32 rows, whose
+    candidates take less room than the latency plan's at 31 rows, so the
+    query never shrinks as n grows."""
+    import _glm53_lib
+    L = _glm53_lib.load()
+    ws = L.glm53_indexer_topk_workspace_bytes
+    assert ws(31, 16384, 512) == 507904
+    assert ws(32, 16384, 512) >= 507904
+    for max_len, k in ((16384, 512), (65536, 512), (262144, 512), (65536, 2048), (20000, 100)):
+        sizes = [ws(n, max_len, k) for n in range(1, 80)]
+        assert all(b >= a for a, b in zip(sizes, sizes[1:])), (max_len, k)
+
+
+def test_attention_token_limit():
+    """Query tokens are the split kernel's grid y: every attention entry
+    point rejects more than 65535 with GLM53_ERR_BAD_SHAPE before anything is
+    launched (the Python wrappers cut larger calls into ranges)."""
+    import _glm53_lib
+    L = _glm53_lib.load()
+    fake = ctypes.c_void_p(0x10000)
+    T = 65536
+    assert L.glm53_sparse_mla(fake, 8192, 512, fake, 528, 10, fake, 2176, T, 16, 2176, 0.04, 4,
+                              fake, 1 << 40, fake, 8192, 512, None) == -2
+    assert L.glm53_sparse_mla_noalloc(fake, 8192, 512, fake, 528, 10, fake, 2176, T, 16, 2176, 0.04, 1,
+                                      fake, 8192, 512, None) == -2
+    assert L.glm53_sparse_mla_partials(fake, 8192, 512, fake, 528, 10, fake, 2176, T, 16, 2176, 0.04, 4,
+                                       fake, 1 << 40, None) == -2
+    assert L.glm53_sparse_mla_gather_floor(fake, 8192, 512, fake, 528, 10, fake, 2176, T, 16, 2176, 4,
+                                           fake, 1 << 40, None) == -2
+    assert L.glm53_sparse_mla_paged(fake, 8192, 512, fake, 33792, 528, 10, fake, 2176, fake, fake, 1, 4, 4, 64,
+                                    T, 16, 2176, 0.04, 4, fake, 1 << 40, fake, 8192, 512, None) == -2
+    assert L.glm53_sparse_mla_pooled(fake, 8192, 512, fake, 33792, 528, 10, fake, 512, 512, None, 4,
+                                     fake, fake, 1, 4, 4, 64, T, 16, 2176, 0.04, 4, fake, 1 << 40,
+                                     fake, 8192, 512, None) == -2
