@@ -35,3 +35,14 @@ def cuda():
 def log_case(*parts):
     """Print (and flush) what names the case before a GPU step."""
     print("[case]", *parts, flush=True)
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The parity magnitudes the GPU tests recorded (parity_log), after the
+    test results, so that the end of the run's output carries them."""
+    import parity_log
+    lines = parity_log.summary_lines()
+    if lines:
+        terminalreporter.write_sep("-", "parity against the oracle")
+        for line in lines:
+            terminalreporter.write_line(line)

@@ -1,14 +1,18 @@
 """The bar the GPU tests hold the sparse MLA outputs to (bf16 attention
 output against the oracle's bf16 output): north_star's mean-abs <= 2e-3 and
 per element |err| <= 2e-2, except on rare elements (at most
-max(2, n / 100000)) of magnitude |ref| >= 2, which may differ by up to two
-bf16 ulps of the reference value: rounding flips of the bf16 output and of a
-dominant key's bf16(p * scale) operand, which any change of fp32 summation
-order causes now and then (the reference's own arithmetic dealt to two
-streams instead of one does it on the CPU:
+max(2, n / 100000)) of magnitude |ref| >= 2, which may differ by up to
+max_ulp (default two) bf16 ulps of the reference value: rounding flips of
+the bf16 output and of a dominant key's bf16(p * scale) operand, which any
+change of fp32 summation order causes now and then (the reference's own
+arithmetic dealt to two streams instead of one does it on the CPU:
 tests/test_oracle.py::test_literal_bar_breaks_under_reordering).  Above
-|ref| = 4 a single ulp is already more than 2e-2."""
+|ref| = 4 a single ulp is already more than 2e-2.  Every comparison is
+recorded (parity_log) with whether it held the literal flat bar or needed
+the exception; the run's summary lists them."""
 import numpy as np
+
+import parity_log
 
 MAX_ABS = 2e-2
 MEAN_ABS = 2e-3
@@ -20,21 +24,25 @@ def bf16_ulp(v):
     return np.exp2(np.floor(np.log2(a)) - 7)
 
 
-def check_bar(got, want, tag):
+def check_bar(got, want, tag, config=None, max_ulp=2):
     """got, want: float32 arrays of one shape (bf16 values widened).  Prints
-    the observed errors and asserts the bar; returns (max-abs, mean-abs)."""
+    and records the observed errors and asserts the bar; returns (max-abs,
+    mean-abs).  config labels a benchmark configuration (parity_log.CONFIGS)."""
     err = np.abs(got - want)
     ulp = bf16_ulp(want)
     over = err > MAX_ABS
     n_over = int(over.sum())
+    worst_ulp = float((err[over] / ulp[over]).max()) if n_over else 0.0
     extra = ""
     if n_over:
         extra = (f" | {n_over} of {err.size} over 2e-2: |ref| {np.abs(want[over]).min():.3g}.."
-                 f"{np.abs(want[over]).max():.3g}, at most {float((err[over] / ulp[over]).max()):.3g} bf16 ulp")
+                 f"{np.abs(want[over]).max():.3g}, at most {worst_ulp:.3g} bf16 ulp")
     print(f"[cmp] {tag}: max|ref| {np.abs(want).max():.3g} max-abs {err.max():.3g} "
           f"mean-abs {err.mean():.3g}{extra}", flush=True)
+    parity_log.record_attention(tag, config, float(err.max()), float(err.mean()), n_over, int(err.size), worst_ulp,
+                                MAX_ABS, MEAN_ABS)
     assert np.isfinite(got).all(), tag
     assert err.mean() <= MEAN_ABS, (tag, float(err.mean()))
-    assert np.all(err[over] <= 2 * ulp[over]) and np.all(np.abs(want[over]) >= 2), (tag, float(err.max()))
+    assert np.all(err[over] <= max_ulp * ulp[over]) and np.all(np.abs(want[over]) >= 2), (tag, float(err.max()))
     assert n_over <= max(2, err.size // 100000), (tag, n_over)
     return float(err.max()), float(err.mean())

@@ -9,6 +9,7 @@ import torch
 
 import workloads as W
 from conftest import log_case
+from parity_log import record_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -53,15 +54,21 @@ def test_random_and_invalid_routes(cuda, oracle):
 
 
 def test_distinct_topk_and_adversarial(cuda, oracle):
+    from titan_moe_align import titan_moe_align_small
     g = W.gen(cuda, W.SEED_BENCH)
     for batch in (1, 2, 4, 8):
         log_case("moe distinct/adversarial", batch)
         ids = W.moe_routes(batch, cuda, g)
-        _check(ids, oracle.moe_align(ids.cpu().numpy()))
         shared = torch.arange(8, device=cuda, dtype=torch.int32).repeat(batch, 1)
-        want = oracle.moe_align(shared.cpu().numpy())
-        assert want[2][0] == 64
-        _check(shared, want)
+        for case, routes in (("distinct top-8", ids), ("shared top-8", shared)):
+            want = oracle.moe_align(routes.cpu().numpy())
+            got = [t.cpu().numpy() for t in titan_moe_align_small(routes)]
+            record_exact("cfg2", f"MoE align {case} (sorted_ids, expert_ids, padded count)",
+                         sum(int(np.count_nonzero(a != b)) if a.shape == b.shape else a.size
+                             for a, b in zip(got, want)), sum(b.size for b in want))
+            if case == "shared top-8":
+                assert want[2][0] == 64
+            _check(routes, want)
 
 
 def test_graph_replay(cuda, oracle):

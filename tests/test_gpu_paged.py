@@ -120,7 +120,7 @@ def test_paged_attention(cuda, oracle, splits, block_size, page_bytes):
         lc = pages_np[btn[reqn[t]]].reshape(-1, 528)
         li = np.where((idxn[t] >= 0) & (idxn[t] < lc.shape[0]), idxn[t], -1)[None, :]
         want = bf16_to_f32(oracle.sparse_mla(qn[t:t + 1], lc, li, W.SM_SCALE, n_splits=1))[0]
-        check_bar(got[t], want, f"paged token {t}")
+        check_bar(got[t], want, f"paged token {t}", max_ulp=1)   # this test's bar held one ulp before the shared bar
 
 
 def test_paged_random_shapes(cuda):

@@ -55,10 +55,10 @@ def f32(u):
     return bf16_to_f32(u)
 
 
-def compare(out, want_u16, tag):
+def compare(out, want_u16, tag, config=None):
     """The attention bar of mla_bar.check_bar, for a HIP output tensor against
-    the oracle's bf16 bits."""
-    return check_bar(out.float().cpu().numpy(), f32(want_u16), tag)
+    the oracle's bf16 bits (config: the benchmark configuration it covers)."""
+    return check_bar(out.float().cpu().numpy(), f32(want_u16), tag, config=config)
 
 
 def textbook_check(out, ref64, tag):
@@ -92,7 +92,7 @@ def test_small_b1_splits(cuda, oracle, small_cache, splits):
     torch.cuda.synchronize()
     want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=splits,
                              groups=kernel_groups(w["idx"].shape[-1], splits), block_n=BLOCK, lazy=LAZY)
-    mx, mean = compare(out, want, f"splits={splits}")
+    mx, mean = compare(out, want, f"splits={splits}", config="cfg1")
     assert mean < 1e-4        # ~bf16 ulp-level agreement
 
 
@@ -286,7 +286,7 @@ def test_full_context_b1_b8(cuda, oracle, full_cache):
             want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s,
                                      nthreads=oracle.default_threads(), groups=kernel_groups(idx.shape[-1], s),
                                      block_n=BLOCK, lazy=LAZY)
-            compare(out, want, (name, splits))
+            compare(out, want, (name, splits), config="cfg4" if name == "b8" else None)
             ref64 = oracle.sparse_mla_f64(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE,
                                           nthreads=oracle.default_threads())
             textbook_check(out, ref64, (name, splits))
@@ -311,7 +311,7 @@ def test_prefill_shaped_sampled(cuda, oracle, full_cache):
     want = oracle.sparse_mla(qs, rows, ids, W.SM_SCALE, n_splits=1, nthreads=oracle.default_threads(),
                              groups=kernel_groups(idx.shape[-1], 1), block_n=BLOCK, lazy=LAZY)
     got = out[torch.as_tensor(pick, device=cuda)]
-    compare(got, want, "prefill sample")
+    compare(got, want, "prefill sample", config="cfg5")
 
 
 # ---------------------------------------------------------------- the reference's own reduction
@@ -326,7 +326,7 @@ def ref_splits(tokens):
     return _choose_num_kv_splits(tokens, 1, W.TOPK, REF_SM_COUNT)
 
 
-def check_reference_reduction(oracle, outs, q, rows, idx, tag):
+def check_reference_reduction(oracle, outs, q, rows, idx, tag, config=None):
     """Every GPU output in `outs` against the reference's single-stream
     reduction at both autotuned tile widths and the reference's split count."""
     s = ref_splits(q.shape[0])
@@ -335,7 +335,7 @@ def check_reference_reduction(oracle, outs, q, rows, idx, tag):
         want = oracle.sparse_mla(qn, rows, ixn, W.SM_SCALE, n_splits=s, groups=1, block_n=block_n,
                                  nthreads=oracle.default_threads())
         for name, out in outs.items():
-            compare(out, want, (tag, name, f"reference splits={s} BLOCK_N={block_n}"))
+            compare(out, want, (tag, name, f"reference splits={s} BLOCK_N={block_n}"), config=config)
 
 
 def test_reference_reduction_small(cuda, oracle, small_cache):
@@ -349,7 +349,7 @@ def test_reference_reduction_small(cuda, oracle, small_cache):
             "reference splits": triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE,
                                                             num_kv_splits=ref_splits(1))}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, w["q"], rows, w["idx"], "small B1")
+    check_reference_reduction(oracle, outs, w["q"], rows, w["idx"], "small B1", config="cfg1")
 
 
 @pytest.fixture(scope="module")
@@ -376,7 +376,7 @@ def test_reference_reduction_full_b1(cuda, oracle, normal_cache):
     outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE),
             "reference splits": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=ref_splits(1))}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, q, rows, idx, "full B1")
+    check_reference_reduction(oracle, outs, q, rows, idx, "full B1", config="cfg3")
 
 
 @pytest.mark.slow
@@ -392,7 +392,7 @@ def test_reference_reduction_full_b8(cuda, oracle, full_cache):
     outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE),
             "reference splits": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=ref_splits(8))}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, q, rows, idx, "full B8")
+    check_reference_reduction(oracle, outs, q, rows, idx, "full B8", config="cfg4")
 
 
 @pytest.mark.slow
@@ -409,7 +409,7 @@ def test_reference_reduction_prefill_all_tokens(cuda, oracle, full_cache):
     log_case("mla prefill-shaped T=2048, all tokens, vs the reference reduction")
     outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE)}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, q, rows, idx, "prefill T=2048")
+    check_reference_reduction(oracle, outs, q, rows, idx, "prefill T=2048", config="cfg5")
 
 
 def test_merge_beyond_register_splits(cuda, oracle, small_cache):

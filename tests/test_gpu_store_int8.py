@@ -5,6 +5,7 @@ import torch
 
 import workloads as W
 from conftest import log_case
+from parity_log import record_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -25,6 +26,7 @@ def test_writer_small_bit_exact(cuda, oracle):
     torch.cuda.synchronize()
     got = u8(w["cache"]).reshape(-1, 528)
     want = oracle.quantize_rows(u16(w["x"]), nthreads=oracle.default_threads())
+    record_exact("cfg1", "store_int8 rows (bytes)", np.count_nonzero(got != want), got.size)
     assert np.array_equal(got, want)
 
 
@@ -148,6 +150,8 @@ def test_full_context_writer_bit_exact(cuda, oracle):
         torch.cuda.synchronize()
         got = u8(cache).reshape(-1, 528)
         want = oracle.quantize_rows(u16(x), nthreads=oracle.default_threads())
+        record_exact("cfg3" if dist == "normal" else "cfg4", "store_int8 rows (bytes)",
+                     np.count_nonzero(got != want), got.size)
         assert np.array_equal(got, want), dist
         del x, cache
         torch.cuda.empty_cache()
@@ -171,7 +175,10 @@ def test_prefill_scattered_writer_full_size(cuda, oracle):
     was = u8(old).reshape(-1, 528)
     s = slots.cpu().numpy()
     want = oracle.quantize_rows(u16(new_rows), nthreads=oracle.default_threads())
-    assert np.array_equal(flat[s], want)
     untouched = np.ones(flat.shape[0], bool)
     untouched[s] = False
+    record_exact("cfg5", "store_int8 scattered rows (bytes)", np.count_nonzero(flat[s] != want), want.size)
+    record_exact("cfg5", "rows not written (bytes changed)", np.count_nonzero(flat[untouched] != was[untouched]),
+                 flat[untouched].size)
+    assert np.array_equal(flat[s], want)
     assert np.array_equal(flat[untouched], was[untouched])
