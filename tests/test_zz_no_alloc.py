@@ -77,3 +77,19 @@ def test_noalloc_equals_workspace_entry(cuda):
     torch.cuda.synchronize()
     assert bool((sentinel == 3.0).all())
     assert b"static scratch" in L.glm53_error_string(ERR_SCRATCH_LIMIT)
+
+
+def test_noalloc_first_call_in_graph_capture(cuda):
+    """The library looks up the device address of its static scratch on the
+    first glm53_sparse_mla_noalloc call on a device; made under HIP graph
+    capture (in a fresh child process, so that no earlier call did the
+    lookup), that call must capture correctly: two replays with different q,
+    each bit-identical to glm53_sparse_mla with a caller workspace."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    child = Path(__file__).resolve().parent / "noalloc_capture_child.py"
+    log_case("noalloc first call under capture (child process)")
+    res = subprocess.run([sys.executable, "-u", str(child)], capture_output=True, text=True, timeout=240)
+    print(res.stdout, res.stderr[-2000:], flush=True)
+    assert res.returncode == 0, res.stdout + res.stderr[-2000:]
