@@ -127,6 +127,26 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def cpu_time(fn, min_s: float, per_call: int = 1) -> float:
+    """The CPU baseline's timing: 3 warm-up calls of fn, then 5 samples, each
+    repeating fn until at least min_s seconds have passed; the median of the
+    samples' mean time per call, in us (fn runs per_call calls each)."""
+    for _ in range(3):
+        fn()
+    samples = []
+    for _ in range(5):
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= min_s:
+                break
+        samples.append(el / (n * per_call) * 1e6)
+    return statistics.median(samples)
+
+
 def split_kernel_threads(topk: int, splits: int) -> int:
     """Threads per workgroup of the decode split kernel the library launches
     for this split length: 12 waves (three key groups) for splits of 65-96
@@ -153,7 +173,41 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
     from titan_kv import store_int8
     from titan_mla import triton_mla_sparse_attention, sparse_mla_partials, _choose_num_kv_splits_mi355x
     K, unroll = args.steps, args.unroll
+    if args.case == "moe_align":
+        # the reference's protocol: 16 calls per graph, median of 5 samples of 100 replays
+        from titan_moe_align import titan_moe_align_small
+        ids = W.moe_routes(args.batch, dev, W.gen(dev, W.SEED_BENCH))
+        mg, _ = capture(torch, lambda: titan_moe_align_small(ids), unroll=16)
+        for _ in range(5):
+            mg.replay()
+        us = statistics.median(timer.replay_loop(mg, 100) / 16 for _ in range(5))
+        log(f"case moe_align B={args.batch}: {us:.3f} us per call (16 per graph, median of 5 x 100 replays)")
+        return
+    if args.case == "dispatch_floor":
+        # a kernel that adds 1 to one int32, 16 per graph: the MoE align protocol's floor
+        one = torch.zeros(1, dtype=torch.int32, device=dev)
+        fg, _ = capture(torch, lambda: one.add_(1), unroll=16)
+        for _ in range(5):
+            fg.replay()
+        us = statistics.median(timer.replay_loop(fg, 100) / 16 for _ in range(5))
+        log(f"case dispatch_floor: {us:.3f} us per kernel (16 per graph, median of 5 x 100 replays)")
+        return
+    if args.case == "copy":
+        # the same box's device copy: the practical HBM ceiling (read + write bytes)
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(3)
+        dst = torch.empty_like(src)
+        cg, _ = capture(torch, lambda: dst.copy_(src), unroll=3)
+        cg.replay()
+        us = timer.median_loop(cg, 5) / 3
+        log(f"case copy: 1 GiB device copy {us:.1f} us, {2 * (1 << 30) / (us * 1e-6) / 1e9:.1f} GB/s (read + write)")
+        return
     caches = [kv8]
+    if args.case in ("decode_b1", "decode_b1_split"):
+        g1, x1, cache1, slots1 = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
+        store_int8(x1, cache1, slots1)
+        del x1
+        q1, idx1 = W.decode_b1_inputs(dev, g1)
+        caches = [cache1.view(n_rows, 1, W.ROW_BYTES)]
     for li in range(1, max(1, args.rotate)):
         _, xr, cr, sr = W.decode_cache(dev, seed=W.SEED_BENCH + 300 + li, dist="t3")
         store_int8(xr, cr, sr)
@@ -174,13 +228,32 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
         fn = lambda: triton_mla_sparse_attention(qp, next_cache(), idxp, W.SM_SCALE, num_kv_splits=args.splits)
         nbytes = W.mla_bytes(idxp, n_rows)
     elif args.case == "decode_b1":
-        g1, x1, cache1, slots1 = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
-        store_int8(x1, cache1, slots1)
-        del x1
-        q1, idx1 = W.decode_b1_inputs(dev, g1)
-        kv1 = cache1.view(n_rows, 1, W.ROW_BYTES)
-        fn = lambda: triton_mla_sparse_attention(q1, kv1, idx1, W.SM_SCALE, num_kv_splits=args.splits)
+        # the B=1 step (split + merge)
+        fn = lambda: triton_mla_sparse_attention(q1, next_cache(), idx1, W.SM_SCALE, num_kv_splits=args.splits)
         nbytes = W.mla_bytes(idx1, n_rows)
+    elif args.case == "decode_b1_split":
+        # the B=1 split kernel alone at the auto split count
+        s1 = args.splits or _choose_num_kv_splits_mi355x(1, 1, W.TOPK, cu)
+        fn = lambda: sparse_mla_partials(q1, next_cache(), idx1, W.SM_SCALE, s1)
+        nbytes = W.mla_bytes(idx1, n_rows)
+    elif args.case == "decode_b8":
+        # the B=8 step (split + merge), the headline's call
+        fn = lambda: triton_mla_sparse_attention(q8, next_cache(), idx8, W.SM_SCALE, num_kv_splits=args.splits)
+        nbytes = W.mla_bytes(idx8, n_rows)
+    elif args.case == "writer_rotation":
+        # store_int8 of 262144 N(0,1) rows, cycling over `rotate` latent/cache sets
+        sets = []
+        for li in range(max(1, args.rotate)):
+            _, xw, cw, sw = W.decode_cache(dev, seed=W.SEED_BENCH + 500 + li, dist="normal")
+            sets.append((xw, cw, sw))
+        turn_w = [0]
+
+        def fn():
+            turn_w[0] += 1
+            xw, cw, sw = sets[(turn_w[0] - 1) % len(sets)]
+            return store_int8(xw, cw, sw)
+        caches = sets
+        nbytes = W.writer_bytes(n_rows)
     elif args.case == "indexer_prefill":
         # 2048 query rows at the end of a 262144-token context: logits over
         # 65536 pools, then the top 512 per row
@@ -216,12 +289,16 @@ def main():
     ap.add_argument("--rotate", type=int, default=1,
                     help="with --case prefill / decode_b8_split: cycle the calls over this many 262144-row "
                          "caches (HBM-resident when their total exceeds the 256 MB MALL)")
-    ap.add_argument("--case", choices=("writer_scattered", "prefill", "decode_b1", "decode_b8_split",
-                                       "indexer_prefill"),
+    ap.add_argument("--case", choices=("writer_scattered", "writer_rotation", "prefill", "decode_b1",
+                                       "decode_b1_split", "decode_b8", "decode_b8_split", "indexer_prefill",
+                                       "moe_align", "dispatch_floor", "copy"),
                     default=None,
                     help="time one workload alone (K calls, one per graph replay unless --unroll), print "
                          "its figure to stderr and exit: the command behind a kernel profile")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--batch", type=int, default=8, choices=(1, 2, 4, 8), help="tokens for --case moe_align")
+    ap.add_argument("--cpu-sample-s", type=float, default=1.0,
+                    help="minimum length of one CPU-baseline timing sample (seconds)")
     ap.add_argument("--splits", type=int, default=None, help="force num_kv_splits for the decode calls")
     ap.add_argument("--sweep", action="store_true",
                     help="print a decode latency table over split counts (stderr) and exit")
@@ -390,11 +467,42 @@ def main():
         us_w = timer.replay_loop(wg, max(5, K // 10))
         us_w_cold = timer.cold_loop(wg, 10, flush)
         wb = W.writer_bytes(x1.shape[0])
-        extra["store_int8_262144"] = {"us_per_call_warm": round(us_w, 2), "us_per_call_cold": round(us_w_cold, 2),
-                                      "algorithmic_bytes": wb, "gbs_warm": round(wb / (us_w * 1e-6) / 1e9, 1),
-                                      "gbs_cold": round(wb / (us_w_cold * 1e-6) / 1e9, 1),
-                                      "hbm_frac_cold": round(wb / (us_w_cold * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
         del wg
+        # HBM-resident: three calls per graph cycling over three latent/cache
+        # sets (3 x 406 MB, more than the 256 MB MALL), no flush inside the
+        # sample; beside it the same box's device copy (1 GiB -> 1 GiB, read +
+        # write bytes) as the practical ceiling of a streaming kernel.
+        wsets = [(x1, cache1, slots1)]
+        for li in range(2):
+            _, xw, cw, sw = W.decode_cache(dev, seed=W.SEED_BENCH + 500 + li, dist="normal")
+            wsets.append((xw, cw, sw))
+        wgr, _ = capture(torch, lambda: [store_int8(xw, cw, sw) for xw, cw, sw in wsets])
+        wgr.replay()
+        us_w_rot = timer.median_loop(wgr, max(2, K // 10)) / len(wsets)
+        del wgr, wsets
+        csrc = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(3)
+        cdst = torch.empty_like(csrc)
+        cgr, _ = capture(torch, lambda: cdst.copy_(csrc), unroll=3)
+        cgr.replay()
+        us_copy = timer.median_loop(cgr, 5) / 3
+        copy_gbs = 2 * (1 << 30) / (us_copy * 1e-6) / 1e9
+        del cgr, csrc, cdst
+        gbs_w_rot = wb / (us_w_rot * 1e-6) / 1e9
+        extra["store_int8_262144"] = {"us_per_call_hbm_rotation": round(us_w_rot, 2),
+                                      "us_per_call_warm": round(us_w, 2), "us_per_call_cold": round(us_w_cold, 2),
+                                      "algorithmic_bytes": wb, "gbs_hbm_rotation": round(gbs_w_rot, 1),
+                                      "hbm_frac_rotation": round(gbs_w_rot / HBM_PEAK_GBS, 3),
+                                      "device_copy_gbs": round(copy_gbs, 1),
+                                      "frac_of_device_copy": round(gbs_w_rot / copy_gbs, 3),
+                                      "gbs_warm": round(wb / (us_w * 1e-6) / 1e9, 1),
+                                      "gbs_cold": round(wb / (us_w_cold * 1e-6) / 1e9, 1),
+                                      "hbm_frac_cold": round(wb / (us_w_cold * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+                                      "rotation": "3 calls per graph over 3 sets of 262144 N(0,1) rows "
+                                                  "(latents 268 MB + cache 138 MB each), median of 5 samples",
+                                      "device_copy": "torch copy_ of 1 GiB into 1 GiB, 3 per graph, "
+                                                     "(read + write bytes) / time",
+                                      "cold": "1 GiB device write before each call (may leave dirty lines "
+                                              "written back inside the timed call)"}
         kv1 = cache1.view(n_rows, 1, W.ROW_BYTES)
         q1, idx1 = W.decode_b1_inputs(dev, g1)
         del x1
@@ -563,7 +671,7 @@ def main():
         # the 256 MB MALL.  "layer rotation" (the decode case): 8 calls per
         # graph cycling over 4 layers' weights (4 x 1.06 GB) with fresh random
         # routes per call, as consecutive MoE layers read other experts.
-        from titan_moe_w4a16 import fused_moe_w4a16, repack_w4a16
+        from titan_moe_w4a16 import fused_moe_w4a16, repack_w4a16, moe_w4a16_gate_up, moe_w4a16_down
         layers = []
         for li in range(4):
             lay = W.moe_w4a16_layer(dev, seed=W.SEED_BENCH + 100 + li)
@@ -587,13 +695,36 @@ def main():
             log(f"moe w4a16 B={b}")
             us_same = timer.replay_loop(gw, max(2, K // args.unroll // 2)) / args.unroll
             us_rot = timer.replay_loop(gr, max(4, K // 8)) / len(calls)
+            del gw, gr
+            # The aligner's cost per layer: the fused layer aligns inside its
+            # gate/up kernel; the same layer as three launches (the aligner
+            # kernel, gate/up over its blocks, down), and as two launches
+            # over alignments computed beforehand (no alignment cost at all).
+            aligned = [titan_moe_align_small(c[1]) for c in calls]
+
+            def staged(c, al=None):
+                al = al if al is not None else titan_moe_align_small(c[1])
+                act = moe_w4a16_gate_up(c[0], c[3][0], c[3][1], al[0], al[1])
+                return moe_w4a16_down(act, c[3][2], c[3][3], c[2], c[1])
+            gsep, _ = capture(torch, lambda: [staged(c) for c in calls], 1)
+            gpre, _ = capture(torch, lambda: [staged(c, al) for c, al in zip(calls, aligned)], 1)
+            for _ in range(3):
+                gsep.replay()
+                gpre.replay()
+            us_sep = timer.replay_loop(gsep, max(4, K // 8)) / len(calls)
+            us_pre = timer.replay_loop(gpre, max(4, K // 8)) / len(calls)
+            del gsep, gpre, aligned
             mb = statistics.mean(W.moe_w4a16_bytes(c[1], b) for c in calls)
             moew[f"B{b}"] = {"us_per_call_same_call": round(us_same, 2),
                              "us_per_call_layer_rotation": round(us_rot, 2),
+                             "us_per_call_layer_rotation_align_kernel_then_gemms": round(us_sep, 2),
+                             "us_per_call_layer_rotation_prealigned_gemms": round(us_pre, 2),
+                             "align_cost_in_fused_layer_us": round(us_rot - us_pre, 2),
+                             "align_cost_as_separate_kernel_us": round(us_sep - us_pre, 2),
                              "algorithmic_bytes_mean": round(mb),
                              "gbs_layer_rotation": round(mb / (us_rot * 1e-6) / 1e9, 1),
                              "hbm_frac_layer_rotation": round(mb / (us_rot * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
-            del gw, gr, calls
+            del calls
         extra["moe_w4a16_layer"] = moew
         del layers
 
@@ -716,28 +847,74 @@ def main():
 
         # ------------------------------------------------------------ CPU baseline
         if not args.no_cpu:
+            # The C oracle on this host's cores (OpenMP over tokens / rows), each
+            # configuration's own inputs, and 1 thread beside it; 3 warm-ups, the
+            # median of 5 samples of at least --cpu-sample-s seconds.
             import oracle
             oracle.build()
-            rows8 = cache8.view(torch.uint8).cpu().numpy().reshape(-1, W.ROW_BYTES)
-            qn = q8.view(torch.int16).cpu().numpy().view(np.uint16)
-            ixn = idx8.cpu().numpy()
             threads = oracle.default_threads()
-            log(f"CPU baseline on {threads} threads")
-            oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=threads)
-            t_cpu = []
-            for _ in range(5):
-                t0 = time.perf_counter()
-                oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=threads)
-                t_cpu.append(time.perf_counter() - t0)
-            us_cpu = statistics.median(t_cpu) * 1e6
-            t0 = time.perf_counter()
-            oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=1)
-            us_cpu1 = (time.perf_counter() - t0) * 1e6
-            cpu = {"value": round(bytes8 / (us_cpu * 1e-6) / 1e9, 3), "unit": "GB/s", "cores": threads,
-                   "kind": "port",
-                   "sample": "the full decode_b8 workload (one B=8 sparse MLA step over the 262144-row cache), "
-                             "median of 5 runs of the C oracle",
-                   "us_per_step": round(us_cpu, 1), "us_per_step_1thread": round(us_cpu1, 1)}
+            ms = args.cpu_sample_s
+            u16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+            rows8 = cache8.view(torch.uint8).cpu().numpy().reshape(-1, W.ROW_BYTES)
+            rows1 = cache1.view(torch.uint8).cpu().numpy().reshape(-1, W.ROW_BYTES)
+            cfgs = {}
+
+            def both(name, fn1, nbytes, unit_note, gpu_us, per_call=1, single_threaded=False):
+                log(f"CPU baseline {name}")
+                row = {}
+                if not single_threaded:
+                    us_n = cpu_time(lambda: fn1(threads), ms, per_call)
+                    row.update(us_per_call=round(us_n, 1), threads=threads,
+                               gbs=round(nbytes / (us_n * 1e-6) / 1e9, 3) if nbytes else None)
+                us_1 = cpu_time(lambda: fn1(1), ms, per_call)
+                row.update(us_per_call_1thread=round(us_1, 2 if us_1 < 100 else 1),
+                           gbs_1thread=round(nbytes / (us_1 * 1e-6) / 1e9, 4) if nbytes else None,
+                           gpu_us_per_call=gpu_us, what=unit_note)
+                cfgs[name] = row
+                return row
+            # cfg3 writer: 262144 N(0,1) rows (the same seeded latents as the GPU's)
+            _, xw, _, _ = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
+            xw_u16 = u16(xw)
+            del xw
+            both("cfg3_store_int8_262144", lambda t: oracle.quantize_rows(xw_u16, nthreads=t), wb,
+                 "store_int8 of 262144 rows into 528-byte rows", extra["store_int8_262144"]["us_per_call_hbm_rotation"])
+            del xw_u16
+            # cfg3 B=1 over the N(0,1) cache
+            q1n, ix1n = u16(q1), idx1.cpu().numpy()
+            both("cfg3_decode_b1", lambda t: oracle.sparse_mla(q1n, rows1, ix1n, W.SM_SCALE, n_splits=s1, nthreads=t),
+                 bytes1, "one B=1 sparse MLA step", extra["decode_b1"]["us_per_step_layer_rotation"])
+            # cfg4 B=8 over the Student-t cache (the headline)
+            qn, ixn = u16(q8), idx8.cpu().numpy()
+            r8 = both("cfg4_decode_b8", lambda t: oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=t),
+                      bytes8, "one B=8 sparse MLA step", round(us8, 3))
+            # cfg5: a sample of 64 of the prefill-shaped call's 2048 tokens
+            pick = np.unique(np.linspace(0, qp.shape[0] - 1, 64).astype(np.int64))
+            qpn, ixpn = u16(qp)[pick], idxp.cpu().numpy()[pick]
+            pbytes = W.mla_bytes(idxp[torch.as_tensor(pick, device=dev)], n_rows)
+            rp = both("cfg5_prefill_64_of_2048_tokens",
+                      lambda t: oracle.sparse_mla(qpn, rows8, ixpn, W.SM_SCALE, n_splits=1, nthreads=t),
+                      pbytes, "64 evenly spaced tokens of the T=2048 call (one split each)",
+                      round(extra["prefill_t2048"]["us_per_call_rotation"] * len(pick) / qp.shape[0], 2))
+            rp["us_per_call_all_2048_tokens_est"] = round(rp["us_per_call"] * qp.shape[0] / len(pick))
+            # cfg2 MoE align B1..8 (the reference's CPU algorithm: a stable
+            # counting sort over the 288 experts; single-threaded), 1000 calls
+            # per timed call through ctypes
+            gm2 = W.gen(dev, W.SEED_BENCH)
+            for b in (1, 2, 4, 8):
+                ids_b = W.moe_routes(b, dev, gm2).cpu().numpy()
+                both(f"cfg2_moe_align_B{b}", lambda t, ids_b=ids_b: oracle.moe_align_repeat(ids_b, 1000), 0,
+                     "one align call (1000 per timed call)", extra["moe_align_us_per_call"][f"B{b}"], per_call=1000,
+                     single_threaded=True)
+            cfgs["host"] = {"threads_used": threads, "os_cpu_count": os.cpu_count(),
+                            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+                            "cpu_model": cpu_model(),
+                            "timing": f"C oracle (-O2, OpenMP), 3 warm-ups, median of 5 samples of >= {ms:g} s each"}
+            extra["cpu_baseline_configs"] = cfgs
+            cpu = {"value": r8["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
+                   "sample": f"the full decode_b8 workload (one B=8 sparse MLA step over the 262144-row cache): "
+                             f"the C oracle on {threads} threads, 3 warm-ups, median of 5 samples of >= {ms:g} s",
+                   "us_per_step": r8["us_per_call"], "us_per_step_1thread": r8["us_per_call_1thread"],
+                   "os_cpu_count": os.cpu_count(), "affinity_cpus": cfgs["host"]["affinity_cpus"]}
 
             # The widened rows' CPU paths (the numpy oracle: float64 reference
             # arithmetic, one call each) beside their GPU figures above.
@@ -789,16 +966,21 @@ def main():
     d = json.loads(tf.read_text())["per_dispatch"].get(key) if tf.exists() else None
     if d:
         traffic = d["fetch_bytes"] + d["write_bytes"]
+        traffic_note = (f"{tf.relative_to(ROOT)} [{key}]: FETCH_SIZE + WRITE_SIZE per dispatch, "
+                        f"{d.get('run', '')}; measured at commit {d.get('commit', 'unrecorded')}")
     else:
         traffic_note = f"no HBM byte measurement for {key} in {tf.relative_to(ROOT)}"
         log(f"WARNING: roofline.traffic is null: {traffic_note}")
+        traffic_note = "null: " + traffic_note
     roofline = {"bound": "hbm", "kernel": "sparse_mla_kernel", "achieved": round(ach, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "algorithmic_bytes": bytes8,
                 "avg_kernel_us": round(us8_kernel, 3),
                 "timing": f"median of {n_samples} samples of {K} launches, HBM-resident (layer rotation)"}
     if traffic_note:
-        roofline["traffic_note"] = traffic_note
+        roofline["traffic_source"] = traffic_note
+    roofline["profile"] = ("profiles/sparse_mla_decode_b8_split_rotation.txt: rocprofv3 kernel trace of this "
+                           "region (bench.py --case decode_b8_split --rotate 5)")
     if cpu is not None:
         cpu["cpu_model"] = cpu_model()
     line = {

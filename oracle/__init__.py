@@ -96,6 +96,7 @@ def lib():
         L.oracle_quantize_row.argtypes = [P, P]
         L.oracle_moe_align.argtypes = [P, I64, P, P, P]
         L.oracle_moe_align_pairwise.argtypes = [P, I64, P, P, P]
+        L.oracle_moe_align_repeat.argtypes = [P, I64, P, P, P, I64]
         L.oracle_sparse_mla.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, F, I64, I64, I64, F, P, I64, I64, I]
         L.oracle_sparse_mla.restype = None
         L.oracle_sparse_mla_f64.argtypes = [P, I64, I64, P, I64, I64, P, I64, I64, I64, I64, D, P, I]
@@ -173,6 +174,17 @@ def moe_align(ids, pairwise: bool = False):
     fn = lib().oracle_moe_align_pairwise if pairwise else lib().oracle_moe_align
     fn(_ptr(flat), R, _ptr(sorted_ids), _ptr(experts), _ptr(postpad))
     return sorted_ids, experts, postpad
+
+
+def moe_align_repeat(ids, iters: int) -> None:
+    """oracle_moe_align `iters` times over the same routes (the CPU
+    baseline's timing loop; outputs discarded)."""
+    flat = np.ascontiguousarray(np.asarray(ids).reshape(-1), dtype=np.int64)
+    R = flat.size
+    sorted_ids = np.empty(R * 8, dtype=np.int32)
+    experts = np.empty(R, dtype=np.int32)
+    postpad = np.empty(1, dtype=np.int32)
+    lib().oracle_moe_align_repeat(_ptr(flat), R, _ptr(sorted_ids), _ptr(experts), _ptr(postpad), int(iters))
 
 
 def moe_patterns(batch: int, rng) -> dict:

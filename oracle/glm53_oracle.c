@@ -116,6 +116,13 @@ void oracle_moe_align(const int64_t* ids, int64_t R, int32_t* sorted,
   for (int64_t b = nb; b < R; b++) experts[b] = -1;
 }
 
+/* The CPU baseline's timing loop: oracle_moe_align `iters` times over the
+ * same routes (one call through ctypes costs about as much as the work). */
+void oracle_moe_align_repeat(const int64_t* ids, int64_t R, int32_t* sorted,
+                             int32_t* experts, int32_t* postpad, int64_t iters) {
+  for (int64_t it = 0; it < iters; it++) oracle_moe_align(ids, R, sorted, experts, postpad);
+}
+
 /* Independent pairwise formulation (rank = earlier routes with the same
  * expert, offset = padded sizes of smaller experts). */
 void oracle_moe_align_pairwise(const int64_t* ids, int64_t R, int32_t* sorted,

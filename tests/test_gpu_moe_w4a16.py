@@ -110,7 +110,7 @@ def test_gate_up_activation_matches_oracle(cuda, oracle, moe, batch):
     """The first kernel alone, fed by the aligner: c2 of every routed slot."""
     import torch
     from titan_moe_align import titan_moe_align_small
-    from titan_moe_w4a16 import moe_w4a16_gate_up, moe_w4a16_down
+    from titan_moe_w4a16 import moe_w4a16_gate_up, moe_w4a16_down, fused_moe_w4a16
     g = torch.Generator(device=cuda).manual_seed(77 + batch)
     x, ids, tw = W.moe_w4a16_inputs(batch, cuda, g)
     ids[0, :3] = ids[0, 4]                      # a shared expert: an aligner block with several slots
@@ -123,6 +123,11 @@ def test_gate_up_activation_matches_oracle(cuda, oracle, moe, batch):
     want_out, want_act = run_oracle(oracle, moe, x, ids, tw)
     assert_act_close(act, want_act, np.arange(batch * 8), oracle, f"B={batch} c2")
     assert_out_close(out, want_out, oracle, f"B={batch} out")
+    # the aligner kernel + two stages and the fused layer (alignment inside
+    # its gate/up kernel) give the same bits
+    fused = fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids)
+    torch.cuda.synchronize()
+    assert torch.equal(out, fused), batch
 
 
 def test_int64_ids_and_invalid_routes(cuda, oracle, moe):
