@@ -227,11 +227,15 @@ __device__ __forceinline__ int pooled_position(PoolAt pool, int num_pools, int p
   return j < seq_len % pool_size ? seq_len / pool_size * pool_size + j : -1;
 }
 
-// V slice element (row, col) in LDS.  Rows are 288 bytes (72 dwords) apart,
-// so the four rows of a ds_read_b64_tr_b16 lane group land on distinct
-// banks; the 16-byte chunks of rows 8-15 of every 16 (row bit 3) are XOR-
-// swapped in pairs so that a 16-byte write of 16 consecutive rows at one
-// column is conflict-free too (without it rows r and r + 8 share banks).
+// V slice element (row, col) in LDS.  The LDS serves 128 bytes (32 banks of
+// 4 bytes) per pass: a ds_read_b64_tr_b16 pass is 16 lanes (4 rows x 32
+// bytes), a ds_write_b128 pass 8 lanes (8 rows x 16 bytes).  Rows are 288
+// bytes (72 dwords, 8 banks) apart, so the four rows of a transposing read
+// land on distinct banks; rows r and r + 4 would then share banks in a
+// write pass, so the 16-byte chunks of rows 4-7 of every 8 (row bit 2) are
+// XOR-swapped in pairs, which the 4-row-aligned reads do not see.  (With
+// the swap on row bit 3 instead, every 16-byte V write cost 8 conflict
+// cycles: SQ_LDS_BANK_CONFLICT, 64 per 32-key tile per wave.)
 // Wave w's parked accumulators: its V buffer holding the wave's 8 MFMA
 // accumulator tiles in register order (float4 of lane l of tile dt at
 // (64 dt + l) * 4): each 16-byte write and read instruction covers 1 KB.
@@ -253,7 +257,7 @@ __device__ __forceinline__ float* part_block(const MlaArgs& a, int t, int split,
 
 template <class Shared>
 __device__ __forceinline__ uint16_t* vbuf_at(Shared& sh, int w, int row, int col) {
-  const int chunk = (col >> 3) ^ ((row >> 3) & 1);
+  const int chunk = (col >> 3) ^ ((row >> 2) & 1);
   return &sh.vbuf[w][row][(chunk << 3) | (col & 7)];
 }
 
@@ -645,11 +649,11 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
 //     gathered the key (ds_bpermute).
 //   * O^T += V^T P^T for the wave's 16 latent tiles; V^T from the wave's bf16
 //     rows in LDS through ds_read_b64_tr_b16.  Rows are 544 bytes (8 banks
-//     apart) and rows 8-15 of every 16 swap the 16-byte halves of each
-//     32-byte block, so both the 16 rows of one write instruction and the 4
-//     rows of each transposing read land on distinct banks, while every
-//     address stays a per-lane base plus a constant (no per-tile address
-//     registers).
+//     apart) and rows 4-7 of every 8 swap the 16-byte halves of each
+//     32-byte block, so both the 8 rows of each write pass and the 4 rows
+//     of each transposing read pass land on distinct banks (the LDS serves
+//     128 bytes per pass), while every address stays a per-lane base plus a
+//     constant (no per-tile address registers).
 //   * The partial S^T buffer is single: a second barrier before a wave
 //     overwrites its half keeps it from racing the other wave's read.
 //   * Gathers run one tile ahead and index loads three, and two waves share
@@ -674,9 +678,9 @@ struct __attribute__((aligned(16))) PairShared {
 };
 
 // Byte offset of bf16 element (row, col) of a wave's V buffer: 16-byte chunk
-// (col / 8) ^ (row / 8 % 2) of the row.
+// (col / 8) ^ (row / 4 % 2) of the row.
 __device__ __forceinline__ int pair_vofs(int row, int col) {
-  return row * kPairRowBytes + 16 * ((col >> 3) ^ ((row >> 3) & 1)) + 2 * (col & 7);
+  return row * kPairRowBytes + 16 * ((col >> 3) ^ ((row >> 2) & 1)) + 2 * (col & 7);
 }
 
 template <int kMode>
