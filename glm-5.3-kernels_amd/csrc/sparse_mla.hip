@@ -255,6 +255,22 @@ __device__ __forceinline__ float* part_block(const MlaArgs& a, int t, int split,
                       (kHeads * kLatent);
 }
 
+// A 16-byte store written through to device scope (cache policy sc1) at
+// byte `off` of the uniform `base`: the key-group kernels' split partials,
+// which the merge kernel reads after the kernel boundary.  Written through,
+// they leave no dirty lines for the boundary's L2 writeback to flush and wait
+// for the merge in the memory-side cache (B=8 over rotating caches 11.40 ->
+// 11.10 us per step, warm 11.16 -> 10.77, B=4 10.39 -> 10.25, paged B=8 11.85
+// -> 11.61 against non-temporal stores; plain stores, sc0 + sc1 and
+// non-temporal + sc1 measured alike or slower; the one-key-group kernel's
+// partials keep plain stores, its B=1 step did not gain).
+__device__ __forceinline__ void store_through(float* base, int off, const float4 v) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, kHeads * kLatent * 4, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(
+      u32x4{__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)}, r, off, 0,
+      16 /* sc1 */);
+}
+
 template <class Shared>
 __device__ __forceinline__ uint16_t* vbuf_at(Shared& sh, int w, int row, int col) {
   const int chunk = (col >> 3) ^ ((row >> 2) & 1);
@@ -606,7 +622,6 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
   // at most one fp32 ulp before the bf16 / fp32 store).
   const float inv_l = 1.f / (l > 0.f ? l : 1.f);
   const bool direct = a.num_splits == 1 && !a.partials_only;
-  float* pb = part_block(a, t, split, hg) + (8 * sl * 64 + lane) * 4;
 #pragma unroll
   for (int dt = 0; dt < 8; dt++) {
     if (owner(dt) != kg) continue;   // uniform across the wave
@@ -625,8 +640,7 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
         *reinterpret_cast<uint2*>(a.out + t * a.so_t + head * a.so_h + col) =
             make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
     } else {
-      // streaming stores: the merge kernel reads each partial once
-      __builtin_nontemporal_store(f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4*>(pb + dt * 64 * 4));
+      store_through(part_block(a, t, split, hg), ((8 * sl + dt) * 64 + lane) * 16, v);
     }
   }
   if (!direct && head_ok && kg == 0 && sl == 0 && g == 0)
