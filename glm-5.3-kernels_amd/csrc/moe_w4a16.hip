@@ -376,6 +376,19 @@ __global__ __launch_bounds__(kThreads) void moe_w4a16_gate_up_kernel(const GateU
     gate_up_dispatch<false>(sh, a, e, jt0, jt_end, slot, xs, c_lo, cpw, k_chunks, t, w, lane, col);
 }
 
+// Weight codes and scales are read once per call: the decode kernels load
+// them non-temporally (nt), which streams faster than plain loads (layer over
+// a 4-layer weight rotation, gate/up and down both nt: B=8 44.8 -> 41.6 us,
+// B=4 27.4 -> 25.1, B=2 16.9 -> 15.8, B=1 12.2 -> 11.6; bit-identical).
+__device__ __forceinline__ uint4 load_once(const uint4* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 load_once(const uint2* p) {
+  const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+  return make_uint2(v.x, v.y);
+}
+
 // ------------------------------------------------------------------ gate/up, streaming
 // For K = 4096 (1..8 tokens at the decode shape): the waves of workgroup
 // (b, g) are kTiles tile pairs x kKSplit parts of K, chosen so that about one
@@ -429,10 +442,10 @@ __device__ __forceinline__ void stream_chunks(const uint16_t* xs, const uint4* w
     }
     if (c + kStreamDepth < kCpw) {   // refill the slot just used (static condition)
       const int cn = c0 + c + kStreamDepth;
-      ring.kg[r] = wg[64 * cn + lane];
-      ring.ku[r] = wu[64 * cn + lane];
-      ring.scg[r] = sg[16 * cn + col];
-      ring.scu[r] = su[16 * cn + col];
+      ring.kg[r] = load_once(&wg[64 * cn + lane]);
+      ring.ku[r] = load_once(&wu[64 * cn + lane]);
+      ring.scg[r] = load_once(&sg[16 * cn + col]);
+      ring.scu[r] = load_once(&su[16 * cn + col]);
     }
     // one chunk per scheduling region, its accumulation included: the
     // accumulators are otherwise only needed at the end, and the instruction
@@ -533,10 +546,10 @@ __global__ __launch_bounds__(64 * kTiles * kKSplit) void moe_w4a16_gate_up_strea
   StreamRing ring;
 #pragma unroll
   for (int c = 0; c < kStreamDepth; c++) {
-    ring.kg[c] = wg[64 * (c0 + c) + lane];
-    ring.ku[c] = wu[64 * (c0 + c) + lane];
-    ring.scg[c] = sg[16 * (c0 + c) + col];
-    ring.scu[c] = su[16 * (c0 + c) + col];
+    ring.kg[c] = load_once(&wg[64 * (c0 + c) + lane]);
+    ring.ku[c] = load_once(&wu[64 * (c0 + c) + lane]);
+    ring.scg[c] = load_once(&sg[16 * (c0 + c) + col]);
+    ring.scu[c] = load_once(&su[16 * (c0 + c) + col]);
   }
   __builtin_amdgcn_sched_barrier(0);
   // vmcnt(4 * kStreamDepth): this wave's activation rows have landed in LDS
@@ -594,8 +607,8 @@ __device__ __forceinline__ void load_down_batch(const uint4* wp, const uint16_t*
 #pragma unroll
   for (int u = 0; u < kBatch; u++) {   // chunks past N re-read the last one (not used)
     const int c = c0 + u < k_chunks ? c0 + u : k_chunks - 1;
-    kw[u] = wp[static_cast<int64_t>(c) * 64];
-    sc[u] = *reinterpret_cast<const uint2*>(sp + 64 * c);
+    kw[u] = load_once(&wp[static_cast<int64_t>(c) * 64]);
+    sc[u] = load_once(reinterpret_cast<const uint2*>(sp + 64 * c));
   }
 }
 
