@@ -6,14 +6,17 @@ Headline: sparse NoPE MLA decode at B=8 over a 262144-row INT8 cache with
 triton_mla_sparse_attention; it is captured once in a HIP graph and replayed
 (the reference's protocol, benchmarks/mla.py:38-55): W untimed replays, then K
 timed replays bracketed by device synchronisation, timed with events on the
-stream the kernels run on; by default 10 steps are captured back to back in
-one graph (as decode steps sit inside one captured model step in serving;
---unroll 1 gives the reference's one-call-per-replay figure, also reported).
-`value` is achieved algorithmic GB/s of the step
+stream the kernels run on; by default up to 20 steps (the largest divisor of
+K up to 20) are captured back to back in one graph, as decode steps sit inside
+one captured model step in serving (each graph boundary adds about 4 us to
+the step after it; --unroll 1 gives the reference's one-call-per-replay
+figure, also reported).  `value` is achieved algorithmic GB/s of the step
 (gathered valid 528-byte rows + indices + q + out) with inputs resident in
-HBM; warm = the replayed working set may sit in the 256 MB Infinity Cache, as
-in the reference's measurements; the cold figures flush it (a 1 GiB write)
-before every timed step.
+HBM: consecutive steps read 256 different caches, more rows between two
+visits of one cache than the 256 MB Infinity Cache holds; warm = one cache
+replayed (its rows stay in the Infinity Cache, as in the reference's
+measurements); the cold figures flush it (a 1 GiB write) before every timed
+step.
 
 Extra fields: the B=1 decode, the 262144-row store_int8 writer, the MoE
 align (16 calls per graph, as docs/measurements.json:1445 records), the W4A16
@@ -167,6 +170,58 @@ def capture(torch, fn, unroll: int = 1):
     return g, out
 
 
+# Decode steps over HBM-resident caches: consecutive steps read different
+# layers' caches, as a model's layers do.  A step touches only its own rows
+# (8.8 MB at B=8, 1.1 MB at B=1), so the rotation needs enough caches that the
+# rows touched between two visits of one cache exceed the 256 MB MALL: 256
+# caches of 262144 rows (35 GB of HBM).  With 5 caches (46 MB touched per
+# cycle at B=8) the B=8 step read 11.12 us per step against 11.35 us over 64
+# or 256 caches, its split kernel 7.31 against 7.55 us.
+ROT_CACHES = 256
+
+
+def rotation_caches(torch, W, store_int8, first, n: int, n_rows: int) -> list:
+    """`first` and n - 1 more 262144-row caches: up to four with contents of
+    their own (latents stored by store_int8), the others copies of those at
+    their own addresses (the timing reads rows, the values do not matter)."""
+    caches = [first]
+    for li in range(1, min(n, 5)):
+        _, xr, cr, sr = W.decode_cache(first.device, seed=W.SEED_BENCH + 300 + li, dist="t3")
+        store_int8(xr, cr, sr)
+        del xr
+        caches.append(cr.view(n_rows, 1, W.ROW_BYTES))
+    base = len(caches)
+    for i in range(base, n):
+        caches.append(caches[i % base].clone())
+    torch.cuda.synchronize()
+    return caches
+
+
+class Cycle:
+    """Graphs replayed in turn: each replay() runs the next one.  Graph j of
+    a rotation runs steps unroll*j .. unroll*(j+1) - 1, each step on its own
+    cache, so k replays time exactly k * unroll steps while the steps keep
+    cycling over every cache of the rotation."""
+
+    def __init__(self, graphs):
+        self.graphs, self.i = graphs, 0
+
+    def replay(self):
+        self.graphs[self.i].replay()
+        self.i = (self.i + 1) % len(self.graphs)
+
+
+def rotation_cycle(torch, caches, fn, unroll: int) -> Cycle:
+    """A Cycle of ceil(len(caches) / unroll) graphs of `unroll` calls
+    fn(cache), call i of the cycle on cache i % len(caches)."""
+    n = len(caches)
+    graphs = []
+    for j in range(-(-n // unroll)):
+        g, _ = capture(torch, lambda j=j: [fn(caches[(unroll * j + i) % n]) for i in range(unroll)], 1)
+        graphs.append(g)
+    return Cycle(graphs)
+
+
 def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
     """One workload alone, for kernel profiles (rocprofv3 --kernel-trace /
     --pmc over exactly these dispatches)."""
@@ -201,18 +256,16 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
         us = timer.median_loop(cg, 5) / 3
         log(f"case copy: 1 GiB device copy {us:.1f} us, {2 * (1 << 30) / (us * 1e-6) / 1e9:.1f} GB/s (read + write)")
         return
-    caches = [kv8]
+    first = kv8
     if args.case in ("decode_b1", "decode_b1_split"):
         g1, x1, cache1, slots1 = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
         store_int8(x1, cache1, slots1)
         del x1
         q1, idx1 = W.decode_b1_inputs(dev, g1)
-        caches = [cache1.view(n_rows, 1, W.ROW_BYTES)]
-    for li in range(1, max(1, args.rotate)):
-        _, xr, cr, sr = W.decode_cache(dev, seed=W.SEED_BENCH + 300 + li, dist="t3")
-        store_int8(xr, cr, sr)
-        del xr
-        caches.append(cr.view(n_rows, 1, W.ROW_BYTES))
+        first = cache1.view(n_rows, 1, W.ROW_BYTES)
+    caches = [first]
+    if args.case != "writer_rotation":
+        caches = rotation_caches(torch, W, store_int8, first, max(1, args.rotate), n_rows)
     turn = [0]
 
     def next_cache():
@@ -270,14 +323,24 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
         s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
         fn = lambda: sparse_mla_partials(q8, next_cache(), idx8, W.SM_SCALE, s8)
         nbytes = W.mla_bytes(idx8, n_rows)
-    # one graph of `unroll` calls, each call reading the next cache of the rotation
-    per_graph = max(unroll, len(caches))
-    gr, _ = capture(torch, lambda: [fn() for _ in range(per_graph)], 1)
-    for _ in range(max(1, args.warmup // per_graph)):
+    # graphs of `unroll` calls replayed in turn (the main run's rotation
+    # protocol), each call reading the next cache of the rotation
+    fn()
+    torch.cuda.synchronize()
+    graphs = []
+    for _ in range(-(-len(caches) // unroll)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(unroll):
+                fn()
+        graphs.append(g)
+    torch.cuda.synchronize()
+    gr = Cycle(graphs)
+    for _ in range(max(1, args.warmup // unroll)):
         gr.replay()
-    us = timer.median_loop(gr, max(1, K // per_graph)) / per_graph
+    us = timer.median_loop(gr, max(1, K // unroll)) / unroll
     log(f"case {args.case}: {us:.3f} us per call, {nbytes / (us * 1e-6) / 1e9:.1f} GB/s algorithmic "
-        f"({nbytes} B), {K} calls, {per_graph} per graph, {len(caches)} cache(s)")
+        f"({nbytes} B), {K} calls, {unroll} per graph, {len(graphs)} graph(s), {len(caches)} cache(s)")
 
 
 def main():
@@ -287,8 +350,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only: skip extras and CPU baseline")
     ap.add_argument("--rotate", type=int, default=1,
-                    help="with --case prefill / decode_b8_split: cycle the calls over this many 262144-row "
-                         "caches (HBM-resident when their total exceeds the 256 MB MALL)")
+                    help="with --case: cycle the calls over this many 262144-row caches (or writer sets); "
+                         "decode steps read their rows from HBM with the main run's 256")
     ap.add_argument("--case", choices=("writer_scattered", "writer_rotation", "prefill", "decode_b1",
                                        "decode_b1_split", "decode_b8", "decode_b8_split", "indexer_prefill",
                                        "moe_align", "dispatch_floor", "copy"),
@@ -302,8 +365,9 @@ def main():
     ap.add_argument("--splits", type=int, default=None, help="force num_kv_splits for the decode calls")
     ap.add_argument("--sweep", action="store_true",
                     help="print a decode latency table over split counts (stderr) and exit")
-    ap.add_argument("--unroll", type=int, default=10,
-                    help="decode steps captured back to back per graph (K must be a multiple)")
+    ap.add_argument("--unroll", type=int, default=None,
+                    help="decode steps captured back to back per graph (K must be a multiple; default: the "
+                         "largest divisor of K up to 20)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 256 MiB device copy (the HBM byte-counter calibration) and exit")
     args = ap.parse_args()
@@ -311,6 +375,8 @@ def main():
         print("bench.py measures one GPU: the library runs the hot path at the per-rank shape on a "
               "single MI355X; multi-GPU runs are not part of it.", file=sys.stderr)
         sys.exit(2)
+    if args.unroll is None and args.steps >= 1:
+        args.unroll = max(d for d in range(1, 21) if args.steps % d == 0)
     if args.steps < 1 or args.warmup < 0 or args.unroll < 1 or args.steps % args.unroll:
         ap.error("steps >= 1, warmup >= 0, steps a multiple of unroll")
 
@@ -378,22 +444,15 @@ def main():
 
     # ---------------------------------------------------------------- headline: B=8
     # HBM-resident (the headline): consecutive steps read different layers'
-    # caches, as a model's layers do -- 5 caches of 262144 rows (692 MB, more
-    # than the 256 MB MALL) cycled within each captured graph, same q and
-    # indices per step.  Warm (one cache replayed, MALL-resident, the
+    # caches (ROT_CACHES of them, same q and indices per step), `unroll`
+    # steps per captured graph.  Warm (one cache replayed, MALL-resident, the
     # reference's protocol) is reported beside it.
-    log("building 4 more 262144-row caches for the layer rotation")
-    rot = [kv8]
-    for li in range(4):
-        _, xr, cr, sr = W.decode_cache(dev, seed=W.SEED_BENCH + 300 + li, dist="t3")
-        store_int8(xr, cr, sr)
-        del xr
-        rot.append(cr.view(n_rows, 1, W.ROW_BYTES))
-    torch.cuda.synchronize()
+    log(f"building the {ROT_CACHES}-cache layer rotation")
+    rot = rotation_caches(torch, W, store_int8, kv8, ROT_CACHES, n_rows)
 
     def rotation(fn):
-        """`unroll` calls of fn(cache), cycling over the rotation caches."""
-        return lambda: [fn(rot[i % len(rot)]) for i in range(args.unroll)]
+        """Steps fn(cache) over the rotation, `unroll` per graph."""
+        return rotation_cycle(torch, rot, fn, args.unroll)
 
     def mla_b8(kv=kv8):
         return triton_mla_sparse_attention(q8, kv, idx8, W.SM_SCALE, num_kv_splits=args.splits)
@@ -402,7 +461,7 @@ def main():
     s8 = args.splits or _choose_num_kv_splits_mi355x(8, 1, W.TOPK, cu)
     bytes8 = W.mla_bytes(idx8, n_rows)
     n_samples = 5
-    graph8r, _ = capture(torch, rotation(mla_b8), 1)
+    graph8r = rotation(mla_b8)
     for _ in range(max(1, Wm // args.unroll)):
         graph8r.replay()
     log(f"decode_b8: timing {n_samples} samples of {K} steps (splits={s8}, {args.unroll} per graph, "
@@ -410,7 +469,7 @@ def main():
     us8 = timer.median_loop(graph8r, K // args.unroll, n_samples) / args.unroll
     gbs8 = bytes8 / (us8 * 1e-6) / 1e9
     # the dominant kernel alone (first stage: split attention -> partials), same rotation
-    pgr, _ = capture(torch, rotation(lambda kv: sparse_mla_partials(q8, kv, idx8, W.SM_SCALE, s8)), 1)
+    pgr = rotation(lambda kv: sparse_mla_partials(q8, kv, idx8, W.SM_SCALE, s8))
     for _ in range(max(1, Wm // args.unroll)):
         pgr.replay()
     us8_kernel = timer.median_loop(pgr, K // args.unroll, n_samples) / args.unroll
@@ -430,8 +489,8 @@ def main():
     # grid, index loads, row gathers, partial stores; no arithmetic) + the merge
     from titan_mla import sparse_mla_gather_floor, sparse_mla_merge
     floor_step = lambda kv: sparse_mla_merge(sparse_mla_gather_floor(q8, kv, idx8, s8), 8, 16, s8)
-    fgr, _ = capture(torch, rotation(floor_step), 1)
-    fgk, _ = capture(torch, rotation(lambda kv: sparse_mla_gather_floor(q8, kv, idx8, s8)), 1)
+    fgr = rotation(floor_step)
+    fgk = rotation(lambda kv: sparse_mla_gather_floor(q8, kv, idx8, s8))
     for _ in range(max(1, Wm // args.unroll)):
         fgr.replay()
         fgk.replay()
@@ -547,11 +606,11 @@ def main():
         del gps
 
         # ------------------------------------------------------------ B=1 layer rotation
-        # B=1 over its own cache and the four rotation caches (HBM-resident).
+        # B=1 over its own cache and the other rotation caches (HBM-resident).
         rot1 = [kv1] + rot[1:]
-        grr, _ = capture(torch, lambda: [triton_mla_sparse_attention(q1, rot1[i % len(rot1)], idx1, W.SM_SCALE,
-                                                                     num_kv_splits=args.splits)
-                                         for i in range(args.unroll)], 1)
+        grr = rotation_cycle(torch, rot1, lambda kv: triton_mla_sparse_attention(q1, kv, idx1, W.SM_SCALE,
+                                                                                 num_kv_splits=args.splits),
+                             args.unroll)
         for _ in range(3):
             grr.replay()
         log("decode_b1 layer rotation")
@@ -560,8 +619,8 @@ def main():
         extra["decode_b1"]["gbs_layer_rotation"] = round(bytes1 / (us_r * 1e-6) / 1e9, 1)
         # B=1's floor: its split kernel's memory chain + the merge, same rotation
         from titan_mla import sparse_mla_gather_floor, sparse_mla_merge
-        fg1, _ = capture(torch, lambda: [sparse_mla_merge(sparse_mla_gather_floor(q1, rot1[i % len(rot1)], idx1, s1),
-                                                          1, 16, s1) for i in range(args.unroll)], 1)
+        fg1 = rotation_cycle(torch, rot1, lambda kv: sparse_mla_merge(sparse_mla_gather_floor(q1, kv, idx1, s1),
+                                                                      1, 16, s1), args.unroll)
         for _ in range(3):
             fg1.replay()
         extra["decode_b1"]["us_floor_step_layer_rotation"] = round(
@@ -572,9 +631,9 @@ def main():
         # The first four query tokens of the B=8 workload over the same
         # rotation (four units: each token's splits on two XCDs).
         q4, idx4 = q8[:4].contiguous(), idx8[:4].contiguous()
-        gr4, _ = capture(torch, lambda: [triton_mla_sparse_attention(q4, rot[i % len(rot)], idx4, W.SM_SCALE,
-                                                                     num_kv_splits=args.splits)
-                                         for i in range(args.unroll)], 1)
+        gr4 = rotation_cycle(torch, rot, lambda kv: triton_mla_sparse_attention(q4, kv, idx4, W.SM_SCALE,
+                                                                                num_kv_splits=args.splits),
+                             args.unroll)
         for _ in range(3):
             gr4.replay()
         log("decode_b4 layer rotation")
@@ -980,7 +1039,7 @@ def main():
     if traffic_note:
         roofline["traffic_source"] = traffic_note
     roofline["profile"] = ("profiles/sparse_mla_decode_b8_split_rotation.txt: rocprofv3 kernel trace of this "
-                           "region (bench.py --case decode_b8_split --rotate 5)")
+                           "region (bench.py --case decode_b8_split --rotate 256)")
     if cpu is not None:
         cpu["cpu_model"] = cpu_model()
     line = {
@@ -1002,7 +1061,8 @@ def main():
                    "timing": f"HIP graph replay, {args.unroll} steps per graph, median of {n_samples} samples "
                              f"of {K} steps",
                    "residency": f"HBM: consecutive steps cycle over {len(rot)} caches of 262144 rows "
-                                f"({len(rot) * n_rows * W.ROW_BYTES / 1e6:.0f} MB > the 256 MB MALL); "
+                                f"({len(rot) * bytes8 / 1e6:.0f} MB of rows touched per cycle > the 256 MB "
+                                "MALL); "
                                 "the warm (MALL-resident) figure is extra.decode_b8.us_per_step_warm"},
         "roofline": roofline,
         "cpu_baseline": cpu,
