@@ -178,6 +178,11 @@ def capture(torch, fn, unroll: int = 1):
 # cycle at B=8) the B=8 step read 11.12 us per step against 11.35 us over 64
 # or 256 caches, its split kernel 7.31 against 7.55 us.
 ROT_CACHES = 256
+# W4A16 MoE layer over HBM: calls with fresh routes cycle over 4 layers' expert
+# weights (1.02 GB each); 32 calls per graph read at least 32 x 28 MB (B=1,
+# 8 experts of 3.5 MB) between two visits of one call's experts, more than the
+# MALL holds.
+MOE_ROT_CALLS = 32
 
 
 def rotation_caches(torch, W, store_int8, first, n: int, n_rows: int) -> list:
@@ -237,6 +242,30 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
             mg.replay()
         us = statistics.median(timer.replay_loop(mg, 100) / 16 for _ in range(5))
         log(f"case moe_align B={args.batch}: {us:.3f} us per call (16 per graph, median of 5 x 100 replays)")
+        return
+    if args.case == "moe_layer":
+        # the fused W4A16 MoE layer at --batch tokens, MOE_ROT_CALLS calls per
+        # graph (fresh routes each) over 4 layers' expert weights
+        from titan_moe_w4a16 import fused_moe_w4a16, repack_w4a16
+        layers = []
+        for li in range(4):
+            lay = W.moe_w4a16_layer(dev, seed=W.SEED_BENCH + 100 + li)
+            layers.append(repack_w4a16(lay["w13_packed"], lay["w13_scale"]) +
+                          repack_w4a16(lay["w2_packed"], lay["w2_scale"]))
+            del lay
+        gmw = W.gen(dev, W.SEED_BENCH + args.batch)
+        calls = []
+        for i in range(MOE_ROT_CALLS):
+            xm, idm, twm = W.moe_w4a16_inputs(args.batch, dev, gmw)
+            calls.append((xm, idm, twm, layers[i % 4]))
+        mg, _ = capture(torch, lambda: [fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1])
+                                        for c in calls], 1)
+        for _ in range(3):
+            mg.replay()
+        us = timer.median_loop(mg, max(1, K // len(calls))) / len(calls)
+        mb = statistics.mean(W.moe_w4a16_bytes(c[1], args.batch) for c in calls)
+        log(f"case moe_layer B={args.batch}: {us:.3f} us per call, {mb / (us * 1e-6) / 1e9:.1f} GB/s algorithmic "
+            f"({mb:.0f} B mean), {len(calls)} calls per graph over 4 layers")
         return
     if args.case == "dispatch_floor":
         # a kernel that adds 1 to one int32, 16 per graph: the MoE align protocol's floor
@@ -354,12 +383,13 @@ def main():
                          "decode steps read their rows from HBM with the main run's 256")
     ap.add_argument("--case", choices=("writer_scattered", "writer_rotation", "prefill", "decode_b1",
                                        "decode_b1_split", "decode_b8", "decode_b8_split", "indexer_prefill",
-                                       "moe_align", "dispatch_floor", "copy"),
+                                       "moe_align", "moe_layer", "dispatch_floor", "copy"),
                     default=None,
                     help="time one workload alone (K calls, one per graph replay unless --unroll), print "
                          "its figure to stderr and exit: the command behind a kernel profile")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--batch", type=int, default=8, choices=(1, 2, 4, 8), help="tokens for --case moe_align")
+    ap.add_argument("--batch", type=int, default=8, choices=(1, 2, 4, 8),
+                    help="tokens for --case moe_align / moe_layer")
     ap.add_argument("--cpu-sample-s", type=float, default=1.0,
                     help="minimum length of one CPU-baseline timing sample (seconds)")
     ap.add_argument("--splits", type=int, default=None, help="force num_kv_splits for the decode calls")
@@ -645,30 +675,32 @@ def main():
 
         # ------------------------------------------------------------ paged decode B=8
         # Request-relative indices: vLLM-style conversion + attention (two
-        # launches before the attention's own) against the fused call.
+        # launches before the attention's own) against the fused call, over
+        # the layer rotation (each cache seen as 4096 pages of 64 rows).
         from sparse_utils import flat_kv_row_view, triton_convert_req_index_to_global_index
         from titan_mla import triton_mla_sparse_attention_paged
         pages, qpg, idxpg, reqpg, btpg = W.paged_b8_inputs(dev, g8, cache8)
-        rows_pg, stride_pg = flat_kv_row_view(pages, pages.shape[1])
-        kv_pg = rows_pg.view(-1, 1, W.ROW_BYTES)
+        bs_pg = pages.shape[1]
+        _, stride_pg = flat_kv_row_view(pages, bs_pg)
+        as_pages = lambda kv: kv.view(n_rows // bs_pg, bs_pg, W.ROW_BYTES)
 
-        def paged_two():
+        def paged_two(kv):
             flat = triton_convert_req_index_to_global_index(
-                reqpg, btpg, idxpg.view(8, -1), BLOCK_SIZE=pages.shape[1], BLOCK_STRIDE_ROWS=stride_pg,
+                reqpg, btpg, idxpg.view(8, -1), BLOCK_SIZE=bs_pg, BLOCK_STRIDE_ROWS=stride_pg,
                 NUM_TOPK_TOKENS=idxpg.shape[-1])
-            return triton_mla_sparse_attention(qpg, kv_pg, flat.view(8, 1, -1), W.SM_SCALE,
+            return triton_mla_sparse_attention(qpg, kv, flat.view(8, 1, -1), W.SM_SCALE,
                                                num_kv_splits=args.splits)
 
-        paged_one = lambda: triton_mla_sparse_attention_paged(qpg, pages, idxpg, reqpg, btpg, W.SM_SCALE,
-                                                              num_kv_splits=args.splits)
+        paged_one = lambda kv: triton_mla_sparse_attention_paged(qpg, as_pages(kv), idxpg, reqpg, btpg, W.SM_SCALE,
+                                                                 num_kv_splits=args.splits)
         log("decode_b8 paged")
-        gp2, _ = capture(torch, paged_two, args.unroll)
-        gp1, _ = capture(torch, paged_one, args.unroll)
-        for _ in range(Wm):
+        gp2 = rotation(paged_two)
+        gp1 = rotation(paged_one)
+        for _ in range(max(1, Wm // args.unroll)):
             gp2.replay()
             gp1.replay()
-        us_two = timer.replay_loop(gp2, K // args.unroll) / args.unroll
-        us_one = timer.replay_loop(gp1, K // args.unroll) / args.unroll
+        us_two = timer.median_loop(gp2, K // args.unroll) / args.unroll
+        us_one = timer.median_loop(gp1, K // args.unroll) / args.unroll
         # Indexer output (top-512 pools of 4 tokens + tail): expansion +
         # conversion + attention, against the one pooled call.
         from sparse_utils import expand_pools_and_append_tail
@@ -676,28 +708,29 @@ def main():
         pools_pg, lens_pg = W.pooled_b8_inputs(dev, g8)
         buf_pg = torch.full((8, 2176), -1, dtype=torch.int32, device=dev)
 
-        def pooled_three():
+        def pooled_three(kv):
             exp = expand_pools_and_append_tail(pools_pg, lens_pg, 4)
             buf_pg[:, : exp.shape[1]].copy_(exp)
             flat = triton_convert_req_index_to_global_index(
-                reqpg, btpg, buf_pg, BLOCK_SIZE=pages.shape[1], BLOCK_STRIDE_ROWS=stride_pg, NUM_TOPK_TOKENS=2176)
-            return triton_mla_sparse_attention(qpg, kv_pg, flat.view(8, 1, -1), W.SM_SCALE,
+                reqpg, btpg, buf_pg, BLOCK_SIZE=bs_pg, BLOCK_STRIDE_ROWS=stride_pg, NUM_TOPK_TOKENS=2176)
+            return triton_mla_sparse_attention(qpg, kv, flat.view(8, 1, -1), W.SM_SCALE,
                                                num_kv_splits=args.splits)
 
-        pooled_one = lambda: triton_mla_sparse_attention_pooled(qpg, pages, pools_pg, lens_pg, 4, reqpg, btpg,
-                                                                W.SM_SCALE, num_kv_splits=args.splits)
-        gq3, _ = capture(torch, pooled_three, args.unroll)
-        gq1, _ = capture(torch, pooled_one, args.unroll)
-        for _ in range(Wm):
+        pooled_one = lambda kv: triton_mla_sparse_attention_pooled(qpg, as_pages(kv), pools_pg, lens_pg, 4, reqpg,
+                                                                   btpg, W.SM_SCALE, num_kv_splits=args.splits)
+        gq3 = rotation(pooled_three)
+        gq1 = rotation(pooled_one)
+        for _ in range(max(1, Wm // args.unroll)):
             gq3.replay()
             gq1.replay()
-        us_q3 = timer.replay_loop(gq3, K // args.unroll) / args.unroll
-        us_q1 = timer.replay_loop(gq1, K // args.unroll) / args.unroll
+        us_q3 = timer.median_loop(gq3, K // args.unroll) / args.unroll
+        us_q1 = timer.median_loop(gq1, K // args.unroll) / args.unroll
         extra["decode_b8_paged"] = {"us_per_step_fused": round(us_one, 3),
                                     "us_per_step_convert_then_attend": round(us_two, 3),
                                     "us_per_step_pooled_fused": round(us_q1, 3),
                                     "us_per_step_expand_convert_attend": round(us_q3, 3),
-                                    "block_size": pages.shape[1], "context_per_request": 32768}
+                                    "block_size": bs_pg, "context_per_request": 32768,
+                                    "residency": "layer rotation (HBM)"}
         del gp1, gp2, gq1, gq3
 
         # ------------------------------------------------------------ MoE align
@@ -741,7 +774,7 @@ def main():
         for b in (1, 2, 4, 8):
             gmw = W.gen(dev, W.SEED_BENCH + b)
             calls = []
-            for i in range(8):
+            for i in range(MOE_ROT_CALLS):
                 xm, idm, twm = W.moe_w4a16_inputs(b, dev, gmw)
                 calls.append((xm, idm, twm, layers[i % 4]))
             one = lambda c=calls[0]: fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1])
