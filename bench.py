@@ -227,6 +227,30 @@ def rotation_cycle(torch, caches, fn, unroll: int) -> Cycle:
     return Cycle(graphs)
 
 
+def stream_ceilings(torch, timer, dev, nbytes: int = 1 << 30) -> dict:
+    """The part's streaming rates through glm53_stream_probe (GB/s): 16-byte
+    lane reads of nbytes with plain and with non-temporal loads, and a
+    non-temporal copy of nbytes (read + write bytes counted), each 3 calls
+    per graph, median of 5 samples -- the ceilings the bandwidth-bound
+    kernels are read against."""
+    import _glm53_lib as lib
+    L = lib.load()
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(7)
+    dst = torch.empty_like(src)
+    out = {}
+    for kind, name, moved in ((0, "read", nbytes), (1, "read_nt", nbytes), (2, "copy_nt", 2 * nbytes)):
+        def call(kind=kind):   # the current stream: under graph capture, the capturing one
+            lib.check(L.glm53_stream_probe(kind, src.data_ptr(), dst.data_ptr(), nbytes, lib.stream_handle(dev)),
+                      "glm53_stream_probe")
+        g, _ = capture(torch, call, 3)
+        g.replay()
+        us = timer.median_loop(g, 5) / 3
+        out[f"{name}_gbs"] = round(moved / (us * 1e-6) / 1e9, 1)
+        del g
+    del src, dst
+    return out
+
+
 def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
     """One workload alone, for kernel profiles (rocprofv3 --kernel-trace /
     --pmc over exactly these dispatches)."""
@@ -275,6 +299,11 @@ def run_case(args, torch, W, dev, timer, g8, kv8, cache8, q8, idx8, n_rows, cu):
             fg.replay()
         us = statistics.median(timer.replay_loop(fg, 100) / 16 for _ in range(5))
         log(f"case dispatch_floor: {us:.3f} us per kernel (16 per graph, median of 5 x 100 replays)")
+        return
+    if args.case == "stream":
+        c = stream_ceilings(torch, timer, dev)
+        log(f"case stream: 1 GiB read {c['read_gbs']} GB/s, non-temporal read {c['read_nt_gbs']} GB/s, "
+            f"non-temporal copy {c['copy_nt_gbs']} GB/s (read + write)")
         return
     if args.case == "copy":
         # the same box's device copy: the practical HBM ceiling (read + write bytes)
@@ -383,7 +412,7 @@ def main():
                          "decode steps read their rows from HBM with the main run's 256")
     ap.add_argument("--case", choices=("writer_scattered", "writer_rotation", "prefill", "decode_b1",
                                        "decode_b1_split", "decode_b8", "decode_b8_split", "indexer_prefill",
-                                       "moe_align", "moe_layer", "dispatch_floor", "copy"),
+                                       "moe_align", "moe_layer", "dispatch_floor", "copy", "stream"),
                     default=None,
                     help="time one workload alone (K calls, one per graph replay unless --unroll), print "
                          "its figure to stderr and exit: the command behind a kernel profile")
@@ -576,6 +605,10 @@ def main():
         us_copy = timer.median_loop(cgr, 5) / 3
         copy_gbs = 2 * (1 << 30) / (us_copy * 1e-6) / 1e9
         del cgr, csrc, cdst
+        extra["hbm_stream_ceilings"] = dict(stream_ceilings(torch, timer, dev), device_copy_gbs=round(copy_gbs, 1),
+                                            what="glm53_stream_probe over 1 GiB: plain and non-temporal 16-byte "
+                                                 "lane reads, non-temporal copy (read + write bytes); "
+                                                 "torch's device copy beside")
         gbs_w_rot = wb / (us_w_rot * 1e-6) / 1e9
         extra["store_int8_262144"] = {"us_per_call_hbm_rotation": round(us_w_rot, 2),
                                       "us_per_call_warm": round(us_w, 2), "us_per_call_cold": round(us_w_cold, 2),

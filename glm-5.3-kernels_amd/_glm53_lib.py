@@ -36,6 +36,7 @@ EXPORTED = (
     "glm53_fp8_paged_mqa_logits",
     "glm53_indexer_topk_workspace_bytes",
     "glm53_indexer_topk",
+    "glm53_stream_probe",
 )
 
 _lib = None
@@ -106,6 +107,8 @@ def load():
     L.glm53_indexer_topk_workspace_bytes.argtypes = [I64, I64, I64]
     L.glm53_indexer_topk.restype = I
     L.glm53_indexer_topk.argtypes = [P, I64, P, I64, I64, I64, P, I64, P, I64, P]
+    L.glm53_stream_probe.restype = I
+    L.glm53_stream_probe.argtypes = [I, P, P, I64, P]
     version = L.glm53_abi_version()
     if version != ABI_VERSION:
         raise ImportError(f"{LIB_PATH} has ABI version {version}, expected {ABI_VERSION}")

@@ -14,7 +14,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent
 LIB_NAME = "libglm53_hip.so"
-SOURCES = ["store_int8.hip", "moe_align.hip", "sparse_mla.hip", "moe_w4a16.hip", "indexer.hip"]
+SOURCES = ["store_int8.hip", "moe_align.hip", "sparse_mla.hip", "moe_w4a16.hip", "indexer.hip", "stream_probe.hip"]
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
 # -ffp-contract=off: every fp32 rounding point is the one the source writes.

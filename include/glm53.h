@@ -391,6 +391,21 @@ int glm53_indexer_topk(const float* logits, int64_t sl, const int32_t* lengths,
                        void* workspace, int64_t workspace_bytes,
                        int32_t* out, int64_t so, void* stream);
 
+/*
+ * Diagnostic, no counterpart in the reference: stream `bytes` (a multiple of
+ * 16, both pointers 16-byte aligned) from src with 16-byte lane loads, the
+ * ceilings that bench.py reads the bandwidth-bound kernels against.
+ *   GLM53_PROBE_READ     plain loads, data folded and discarded (dst: one
+ *                        16-byte sink, written only for one magic value)
+ *   GLM53_PROBE_READ_NT  the same with non-temporal loads
+ *   GLM53_PROBE_COPY_NT  copy src -> dst (bytes each) with non-temporal
+ *                        loads and stores
+ */
+#define GLM53_PROBE_READ     0
+#define GLM53_PROBE_READ_NT  1
+#define GLM53_PROBE_COPY_NT  2
+int glm53_stream_probe(int kind, const void* src, void* dst, int64_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -429,3 +429,20 @@ def test_attention_token_limit():
     assert L.glm53_sparse_mla_pooled(fake, 8192, 512, fake, 33792, 528, 10, fake, 512, 512, None, 4,
                                      fake, fake, 1, 4, 4, 64, T, 16, 2176, 0.04, 4, fake, 1 << 40,
                                      fake, 8192, 512, None) == -2
+
+
+def test_stream_probe_argument_checks():
+    """The streaming probe validates before anything is launched: unknown
+    kind, null pointers, sizes that are not a positive multiple of 16 and
+    pointers off 16-byte alignment."""
+    import _glm53_lib
+    L = _glm53_lib.load()
+    a, b = ctypes.c_void_p(0x10000), ctypes.c_void_p(0x20000)
+    assert L.glm53_stream_probe(3, a, b, 1 << 20, None) == -2
+    assert L.glm53_stream_probe(-1, a, b, 1 << 20, None) == -2
+    assert L.glm53_stream_probe(0, None, b, 1 << 20, None) == -1
+    assert L.glm53_stream_probe(2, a, None, 1 << 20, None) == -1
+    assert L.glm53_stream_probe(1, a, b, 8, None) == -2
+    assert L.glm53_stream_probe(1, a, b, (1 << 20) + 4, None) == -2
+    assert L.glm53_stream_probe(0, ctypes.c_void_p(0x10008), b, 1 << 20, None) == -3
+    assert L.glm53_stream_probe(2, a, ctypes.c_void_p(0x20004), 1 << 20, None) == -3
