@@ -413,6 +413,11 @@ struct StreamRing {
 };
 
 // Chunks [c0, c0 + kCpw) of one tile pair; the ring holds chunks c0.. on entry.
+// Per chunk: the four groups' MFMAs back to back (their activations read
+// from LDS one chunk ahead), the ring slot refilled, then the scale FMAs in
+// group order -- the same arithmetic as one group at a time, with fewer
+// waits on LDS reads and MFMA results (B=8 layer 41.19 -> 40.84 us, B=2
+// 15.87 -> 15.63 in an interleaved A/B; bit-identical).
 template <int kCpw>
 __device__ __forceinline__ void stream_chunks(const uint16_t* xs, const uint4* wg, const uint4* wu, const uint2* sg,
                                               const uint2* su, StreamRing& ring, int c0, int lane, f32x4& acc_g,
@@ -420,32 +425,47 @@ __device__ __forceinline__ void stream_chunks(const uint16_t* xs, const uint4* w
   const bf16x8 minus136 = __builtin_bit_cast(bf16x8, make_uint4(kMinus136, kMinus136, kMinus136, kMinus136));
   const uint32_t mask = nibble_mask();
   const int col = lane & 15;
+  bf16x8 xn[4];   // the next chunk's activations, read from LDS one chunk ahead
+#pragma unroll
+  for (int i = 0; i < 4; i++) xn[i] = *reinterpret_cast<const bf16x8*>(xs + kChunkK * c0 + kGroup * i);
 #pragma unroll
   for (int c = 0; c < kCpw; c++) {
     const int r = c % kStreamDepth;
+    bf16x8 xv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) xv[i] = xn[i];
+    if (c + 1 < kCpw) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) xn[i] = *reinterpret_cast<const bf16x8*>(xs + kChunkK * (c0 + c + 1) + kGroup * i);
+    }
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 corr[4], dg[4], du[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) corr[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[i], minus136, zero, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const bf16x8 xv = *reinterpret_cast<const bf16x8*>(xs + kChunkK * (c0 + c) + kGroup * i);
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      const f32x4 corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, minus136, zero, 0, 0, 0);
-      const f32x4 dg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ring.kg[r], i), mask), corr, 0, 0, 0);
-      const f32x4 du = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv, codes_to_bf16(word_of(ring.ku[r], i), mask), corr, 0, 0, 0);
-      const uint32_t pg = i < 2 ? ring.scg[r].x : ring.scg[r].y;
-      const uint32_t pu = i < 2 ? ring.scu[r].x : ring.scu[r].y;
-      const float s_g = __uint_as_float((i & 1) ? (pg & 0xFFFF0000u) : (pg << 16));
-      const float s_u = __uint_as_float((i & 1) ? (pu & 0xFFFF0000u) : (pu << 16));
-#pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        acc_g[rr] = __builtin_fmaf(s_g, dg[rr], acc_g[rr]);
-        acc_u[rr] = __builtin_fmaf(s_u, du[rr], acc_u[rr]);
-      }
+      dg[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[i], codes_to_bf16(word_of(ring.kg[r], i), mask), corr[i], 0, 0, 0);
+      du[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[i], codes_to_bf16(word_of(ring.ku[r], i), mask), corr[i], 0, 0, 0);
     }
+    const uint2 pgs = ring.scg[r], pus = ring.scu[r];
     if (c + kStreamDepth < kCpw) {   // refill the slot just used (static condition)
       const int cn = c0 + c + kStreamDepth;
       ring.kg[r] = load_once(&wg[64 * cn + lane]);
       ring.ku[r] = load_once(&wu[64 * cn + lane]);
       ring.scg[r] = load_once(&sg[16 * cn + col]);
       ring.scu[r] = load_once(&su[16 * cn + col]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t pg = i < 2 ? pgs.x : pgs.y;
+      const uint32_t pu = i < 2 ? pus.x : pus.y;
+      const float s_g = __uint_as_float((i & 1) ? (pg & 0xFFFF0000u) : (pg << 16));
+      const float s_u = __uint_as_float((i & 1) ? (pu & 0xFFFF0000u) : (pu << 16));
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        acc_g[rr] = __builtin_fmaf(s_g, dg[i][rr], acc_g[rr]);
+        acc_u[rr] = __builtin_fmaf(s_u, du[i][rr], acc_u[rr]);
+      }
     }
     // one chunk per scheduling region, its accumulation included: the
     // accumulators are otherwise only needed at the end, and the instruction
