@@ -282,7 +282,7 @@ __device__ __forceinline__ uint16_t* vbuf_at(Shared& sh, int w, int row, int col
 // built to preload the first 16 dwords of scalar arguments into SGPRs, so
 // these arrive with the wave instead of through a scalar load that would
 // head the index -> row chain.
-template <int kMode, bool kPipe, int kG>
+template <int kMode, bool kPipe, int kG, bool kPad = false>
 __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
     const int32_t* idx, int64_t si_t, int split_len, int topk, int grid_x, int grid_y, int grid_z, int num_heads,
     const uint16_t* q, int64_t sq_t, int64_t sq_h, const MlaArgs a) {
@@ -299,16 +299,21 @@ __global__ __launch_bounds__(SplitShape<kG>::kThreads) void sparse_mla_kernel(
   // two XCDs for a multiple of 4 (B=4: token t on XCDs t and t + 4; 10.83
   // -> 10.37 us per call over rotating caches), where the merge kernel
   // reads them back.
-  // (Other unit counts keep the plain mapping: at B=1 the divisions cost
-  // 0.35 us for nothing, and B=2 gains nothing from four XCDs per token.)
+  // kPad: batches of 3, 5, 6 or 7 tokens are numbered as 4 or 8 (grid_y
+  // holds the numbered tokens in its low 16 bits, the batch's in the high
+  // 16); the extra tokens' workgroups return at once.  (B=1 and B=2 keep the
+  // plain mapping: at B=1 the divisions cost 0.35 us for nothing, and B=2
+  // gains nothing from four XCDs per token.)
+  const int gy = kPad ? (grid_y & 0xffff) : grid_y;
   int split = blockIdx.x, t = blockIdx.y, hg = blockIdx.z;
-  if ((grid_y * grid_z) % 4 == 0) {
-    const int lin = blockIdx.x + grid_x * (blockIdx.y + grid_y * blockIdx.z);
-    const int units = grid_y * grid_z;
+  if ((gy * grid_z) % 4 == 0) {
+    const int lin = blockIdx.x + grid_x * (blockIdx.y + gy * blockIdx.z);
+    const int units = gy * grid_z;
     split = lin / units;
-    t = (lin % units) % grid_y;
-    hg = (lin % units) / grid_y;
+    t = (lin % units) % gy;
+    hg = (lin % units) / gy;
   }
+  if (kPad && t >= static_cast<int>(static_cast<unsigned>(grid_y) >> 16)) return;   // uniform
   const int w = uniform(threadIdx.x >> 6);
   const int sl = w & (kSlices - 1);
   const int kg = w / kSlices;
@@ -1099,6 +1104,7 @@ __global__ __launch_bounds__(256) void expand_pools_kernel(const PoolT* __restri
 constexpr int kMergeRegs = 16;   // splits per lane held in registers (S <= 128)
 constexpr int kMergeThreads = kMergeLanes * 64;
 
+template <bool kPad>
 __global__ __launch_bounds__(kMergeThreads) void sparse_mla_merge_kernel(const float* __restrict__ part,
                                                                           const float* __restrict__ lse,
                                                                           int num_splits, int heads_padded,
@@ -1111,15 +1117,19 @@ __global__ __launch_bounds__(kMergeThreads) void sparse_mla_merge_kernel(const f
   // token fastest in the linear id: with a multiple of 8 (4) tokens, token
   // t's workgroups share the XCD (the two XCDs) that ran its splits
   // (num_tokens * groups is gridDim.x, passed in with the leading arguments
-  // so that it arrives preloaded)
+  // so that it arrives preloaded).  kPad: num_tokens holds the numbered
+  // tokens (low 16 bits) and the batch's (high 16), as the split kernel's
+  // grid_y does.
+  const int nt = kPad ? (num_tokens & 0xffff) : num_tokens;
   const int groups = heads_padded / kHeads;
   int t = blockIdx.x / groups, hg = blockIdx.x % groups, tile = blockIdx.y;
-  if (num_tokens % 4 == 0) {
-    const int lin = blockIdx.x + num_tokens * groups * blockIdx.y;
-    t = lin % num_tokens;
-    hg = (lin / num_tokens) % groups;
-    tile = lin / (num_tokens * groups);
+  if (nt % 4 == 0) {
+    const int lin = blockIdx.x + nt * groups * blockIdx.y;
+    t = lin % nt;
+    hg = (lin / nt) % groups;
+    tile = lin / (nt * groups);
   }
+  if (kPad && t >= static_cast<int>(static_cast<unsigned>(num_tokens) >> 16)) return;   // uniform
   const int tid = threadIdx.x;
   const int sp = tid >> 6;          // split lane (one wave each)
   const int p = tid & 63;           // position 16 g + c
@@ -1263,16 +1273,21 @@ int prepare(MlaArgs& a, const void* q, int64_t sq_t, int64_t sq_h, const void* k
   return 0;
 }
 
+// Tokens the split and merge kernels number: 3, 5, 6 or 7 tokens (one head
+// group) as 4 or 8, so that a token's splits share one XCD (two at 4) --
+// when they fit its CUs -- and the merge reads them back there, the extra
+// tokens' workgroups returning at once.  Interleaved A/B over rotating
+// HBM-resident caches, 23 splits: B=5 11.92 -> 11.11 us, B=6 12.05 -> 11.29,
+// B=7 12.25 -> 11.31; B=3 (34 splits) 10.48 -> 10.37; bit-identical.
+int64_t tokens_grid(int64_t num_tokens, int heads_padded, int64_t num_splits) {
+  if (heads_padded != kHeads || num_tokens < 3 || num_tokens > 7 || num_tokens == 4) return num_tokens;
+  const int64_t tp = num_tokens == 3 ? 4 : 8;
+  return num_splits <= 32 * (8 / tp) ? tp : num_tokens;   // each XCD's share within its 32 CUs
+}
+
 void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(num_tokens),
-                  static_cast<unsigned>(a.heads_padded / kHeads));
   // Splits longer than one chunk of gathers pipeline their chunks.
   const bool pipe = a.split_len > kChunkTiles * kTile;
-  const int mode = a.pools != nullptr ? kPooledPos : a.bt != nullptr ? kPagedPos : kFlatRows;
-#define GLM53_LEAD a.idx, a.si_t, a.split_len, a.topk, static_cast<int>(grid.x), static_cast<int>(grid.y), \
-                   static_cast<int>(grid.z), a.num_heads, a.q, a.sq_t, a.sq_h, a
-#define GLM53_LAUNCH(M, P) hipLaunchKernelGGL((sparse_mla_kernel<M, P, 2>), grid, dim3(kThreads), 0, st, GLM53_LEAD)
-#define GLM53_PAIR(M) hipLaunchKernelGGL((sparse_mla_pair_kernel<M>), grid, dim3(128), 0, st, a)
   // Long splits go to the pair kernel, whose masked keys read row 0 (page 0):
   // it needs a non-empty cache (seq_kv counts rows, or pages when paged).
   const bool pair = pipe && a.seq_kv > 0;
@@ -1280,8 +1295,31 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
   // key groups, splits of one tile on one key group.
   const bool three = a.split_len > 2 * kTile && a.split_len <= 3 * kTile;
   const bool one = a.split_len <= kTile;
-#define GLM53_KG(M, G) hipLaunchKernelGGL((sparse_mla_kernel<M, false, G>), grid, \
-                                          dim3(SplitShape<G>::kThreads), 0, st, GLM53_LEAD)
+  const int64_t tg = pipe || one ? num_tokens : tokens_grid(num_tokens, a.heads_padded, a.num_splits);
+  const bool pad = tg != num_tokens;
+  const dim3 grid(static_cast<unsigned>(a.num_splits), static_cast<unsigned>(tg),
+                  static_cast<unsigned>(a.heads_padded / kHeads));
+  const int gy_arg = pad ? static_cast<int>(tg | (num_tokens << 16)) : static_cast<int>(tg);
+  const int mode = a.pools != nullptr ? kPooledPos : a.bt != nullptr ? kPagedPos : kFlatRows;
+#define GLM53_LEAD a.idx, a.si_t, a.split_len, a.topk, static_cast<int>(grid.x), gy_arg, \
+                   static_cast<int>(grid.z), a.num_heads, a.q, a.sq_t, a.sq_h, a
+#define GLM53_LAUNCH(M, P)                                                                        \
+  do {                                                                                            \
+    if (pad && !P)                                                                                \
+      hipLaunchKernelGGL((sparse_mla_kernel<M, P, 2, true>), grid, dim3(kThreads), 0, st, GLM53_LEAD); \
+    else                                                                                          \
+      hipLaunchKernelGGL((sparse_mla_kernel<M, P, 2>), grid, dim3(kThreads), 0, st, GLM53_LEAD);       \
+  } while (0)
+#define GLM53_PAIR(M) hipLaunchKernelGGL((sparse_mla_pair_kernel<M>), grid, dim3(128), 0, st, a)
+#define GLM53_KG(M, G)                                                                                 \
+  do {                                                                                                 \
+    if (pad && G == 3)                                                                                 \
+      hipLaunchKernelGGL((sparse_mla_kernel<M, false, 3, true>), grid, dim3(SplitShape<3>::kThreads), 0, st, \
+                         GLM53_LEAD);                                                                  \
+    else                                                                                               \
+      hipLaunchKernelGGL((sparse_mla_kernel<M, false, G>), grid, dim3(SplitShape<G>::kThreads), 0, st,       \
+                         GLM53_LEAD);                                                                  \
+  } while (0)
   if (mode == kPooledPos) {
     if (pair) GLM53_PAIR(kPooledPos); else if (pipe) GLM53_LAUNCH(kPooledPos, true);
     else if (three) GLM53_KG(kPooledPos, 3); else if (one) GLM53_KG(kPooledPos, 1); else GLM53_LAUNCH(kPooledPos, false);
@@ -1301,9 +1339,14 @@ void launch_attention(const MlaArgs& a, int64_t num_tokens, hipStream_t st) {
 void launch_merge(const float* part, const float* lse, int64_t num_tokens, int num_splits,
                   int heads_padded, int num_heads, uint16_t* out, int64_t so_t, int64_t so_h,
                   hipStream_t st) {
-  hipLaunchKernelGGL(sparse_mla_merge_kernel, dim3(static_cast<unsigned>(num_tokens * (heads_padded / kHeads)), 32),
-                     dim3(kMergeThreads), 0, st, part, lse, num_splits, heads_padded, num_heads,
-                     static_cast<int>(num_tokens), out, so_t, so_h);
+  const int64_t tg = tokens_grid(num_tokens, heads_padded, num_splits);
+  const dim3 grid(static_cast<unsigned>(tg * (heads_padded / kHeads)), 32);
+  if (tg != num_tokens)
+    hipLaunchKernelGGL(sparse_mla_merge_kernel<true>, grid, dim3(kMergeThreads), 0, st, part, lse, num_splits,
+                       heads_padded, num_heads, static_cast<int>(tg | (num_tokens << 16)), out, so_t, so_h);
+  else
+    hipLaunchKernelGGL(sparse_mla_merge_kernel<false>, grid, dim3(kMergeThreads), 0, st, part, lse, num_splits,
+                       heads_padded, num_heads, static_cast<int>(num_tokens), out, so_t, so_h);
 }
 
 }  // namespace

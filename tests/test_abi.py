@@ -115,6 +115,8 @@ def test_library_split_policy_table():
         (2, 1, 2176, 256): 34, (3, 1, 2176, 256): 34, (4, 1, 2176, 256): 34,
         (1, 2, 2176, 256): 34,            # two head groups: two units
         (8, 1, 2176, 256): 23,            # cap 32 -> 3 tiles per split -> ceil(68 / 3) = 23
+        (5, 1, 2176, 256): 23, (6, 1, 2176, 256): 23, (7, 1, 2176, 256): 23,   # sized as 8 tokens
+        (7, 2, 2176, 256): 17,            # two head groups: 14 units, cap 18 -> 4 tiles per split -> 17
         (16, 1, 2176, 256): 14,           # cap 16 -> 5 tiles per split -> 14
         (8, 4, 2176, 256): 8,             # 32 units: cap 8 -> 9 tiles per split -> 8
         (256, 1, 2176, 256): 1, (2048, 1, 2176, 256): 1, (300, 1, 2176, 256): 1,

@@ -257,6 +257,39 @@ def test_xcd_grouped_units(cuda, oracle, small_cache):
         compare(out, want, ("xcd-grouped", T, heads, topk, splits))
 
 
+def test_padded_token_numbering(cuda, oracle, small_cache):
+    """Batches of 3, 5, 6 and 7 tokens (one head group) are numbered as 4 or 8
+    tokens by the split and merge kernels when each token's splits fit its
+    XCDs (the extra tokens' workgroups return at once): the auto split count
+    (34 at 3 tokens, 23 at 5-7), forced counts that still pad (17; 34 at 3)
+    and ones that do not (34 at 5-7: more than one XCD's CUs; one-tile
+    splits), each against the oracle, and the partials + merge path equal to
+    the one call byte for byte."""
+    from titan_mla import (triton_mla_sparse_attention, sparse_mla_partials, sparse_mla_merge,
+                           _choose_num_kv_splits_mi355x)
+    w, rows = small_cache
+    n = w["n_rows"]
+    kv = w["cache"].view(n, 1, 528)
+    rng = np.random.default_rng(909)
+    g = W.gen(cuda, 909)
+    cu = torch.cuda.get_device_properties(cuda).multi_processor_count
+    for T in (3, 5, 6, 7):
+        topk = 2176
+        q = torch.randn(T, 16, 512, generator=g, device=cuda).to(torch.bfloat16)
+        idx = torch.from_numpy(rng.integers(-8, n + 8, size=(T, 1, topk)).astype(np.int32)).to(cuda)
+        auto = _choose_num_kv_splits_mi355x(T, 1, topk, cu)
+        assert auto == (34 if T == 3 else 23)
+        for splits in (auto, 17, 34, 68):
+            log_case("mla padded numbering", T, topk, splits)
+            out = triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=splits)
+            parts = sparse_mla_merge(sparse_mla_partials(q, kv, idx, W.SM_SCALE, splits), T, 16, splits)
+            torch.cuda.synchronize()
+            assert torch.equal(parts, out), ("partials + merge", T, splits)
+            want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=splits,
+                                     groups=kernel_groups(topk, splits), block_n=BLOCK, lazy=LAZY)
+            compare(out, want, ("padded numbering", T, splits))
+
+
 @pytest.fixture(scope="module")
 def full_cache(cuda):
     from titan_kv import store_int8
