@@ -997,37 +997,37 @@ def main():
                            gpu_us_per_call=gpu_us, what=unit_note)
                 cfgs[name] = row
                 return row
-            # cfg3 writer: 262144 N(0,1) rows (the same seeded latents as the GPU's)
+            # the writer: 262144 N(0,1) rows (the same seeded latents as the GPU's)
             _, xw, _, _ = W.decode_cache(dev, seed=W.SEED_BENCH + 1, dist="normal")
             xw_u16 = u16(xw)
             del xw
-            both("cfg3_store_int8_262144", lambda t: oracle.quantize_rows(xw_u16, nthreads=t), wb,
+            both("store_int8_262144_normal", lambda t: oracle.quantize_rows(xw_u16, nthreads=t), wb,
                  "store_int8 of 262144 rows into 528-byte rows", extra["store_int8_262144"]["us_per_call_hbm_rotation"])
             del xw_u16
-            # cfg3 B=1 over the N(0,1) cache
+            # B=1 over the N(0,1) cache
             q1n, ix1n = u16(q1), idx1.cpu().numpy()
-            both("cfg3_decode_b1", lambda t: oracle.sparse_mla(q1n, rows1, ix1n, W.SM_SCALE, n_splits=s1, nthreads=t),
+            both("decode_b1_normal", lambda t: oracle.sparse_mla(q1n, rows1, ix1n, W.SM_SCALE, n_splits=s1, nthreads=t),
                  bytes1, "one B=1 sparse MLA step", extra["decode_b1"]["us_per_step_layer_rotation"])
-            # cfg4 B=8 over the Student-t cache (the headline)
+            # B=8 over the Student-t cache (the headline)
             qn, ixn = u16(q8), idx8.cpu().numpy()
-            r8 = both("cfg4_decode_b8", lambda t: oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=t),
+            r8 = both("decode_b8_t3", lambda t: oracle.sparse_mla(qn, rows8, ixn, W.SM_SCALE, n_splits=s8, nthreads=t),
                       bytes8, "one B=8 sparse MLA step", round(us8, 3))
-            # cfg5: a sample of 64 of the prefill-shaped call's 2048 tokens
+            # a sample of 64 of the prefill-shaped call's 2048 tokens
             pick = np.unique(np.linspace(0, qp.shape[0] - 1, 64).astype(np.int64))
             qpn, ixpn = u16(qp)[pick], idxp.cpu().numpy()[pick]
             pbytes = W.mla_bytes(idxp[torch.as_tensor(pick, device=dev)], n_rows)
-            rp = both("cfg5_prefill_64_of_2048_tokens",
+            rp = both("prefill_64_of_2048_tokens",
                       lambda t: oracle.sparse_mla(qpn, rows8, ixpn, W.SM_SCALE, n_splits=1, nthreads=t),
                       pbytes, "64 evenly spaced tokens of the T=2048 call (one split each)",
                       round(extra["prefill_t2048"]["us_per_call_rotation"] * len(pick) / qp.shape[0], 2))
             rp["us_per_call_all_2048_tokens_est"] = round(rp["us_per_call"] * qp.shape[0] / len(pick))
-            # cfg2 MoE align B1..8 (the reference's CPU algorithm: a stable
+            # MoE align B1..8 (the reference's CPU algorithm: a stable
             # counting sort over the 288 experts; single-threaded), 1000 calls
             # per timed call through ctypes
             gm2 = W.gen(dev, W.SEED_BENCH)
             for b in (1, 2, 4, 8):
                 ids_b = W.moe_routes(b, dev, gm2).cpu().numpy()
-                both(f"cfg2_moe_align_B{b}", lambda t, ids_b=ids_b: oracle.moe_align_repeat(ids_b, 1000), 0,
+                both(f"moe_align_B{b}", lambda t, ids_b=ids_b: oracle.moe_align_repeat(ids_b, 1000), 0,
                      "one align call (1000 per timed call)", extra["moe_align_us_per_call"][f"B{b}"], per_call=1000,
                      single_threaded=True)
             cfgs["host"] = {"threads_used": threads, "os_cpu_count": os.cpu_count(),

@@ -260,7 +260,7 @@ def sparse_mla_f64(q_u16: np.ndarray, rows: np.ndarray, idx: np.ndarray, sm_scal
 
 def default_threads() -> int:
     """Host threads for the oracle: the CPUs this process may run on, at
-    most 16 (a GPU box's CPU share per GPU)."""
+    most 16 (the host CPU share of one GPU on an 8-GPU node)."""
     n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     return max(1, min(16, n))
 

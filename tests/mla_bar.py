@@ -1,5 +1,5 @@
 """The bar the GPU tests hold the sparse MLA outputs to (bf16 attention
-output against the oracle's bf16 output): north_star's mean-abs <= 2e-3 and
+output against the oracle's bf16 output): the target's mean-abs <= 2e-3 and
 per element |err| <= 2e-2, except on rare elements (at most
 max(2, n / 100000)) of magnitude |ref| >= 2, which may differ by up to
 max_ulp (default two) bf16 ulps of the reference value: rounding flips of

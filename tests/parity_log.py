@@ -12,11 +12,11 @@ ATTENTION = []
 EXACT = []
 
 CONFIGS = {
-    "cfg1": "16384-row cache, B=1, 2048 uniform + 128 pads",
-    "cfg2": "MoE align, distinct top-8 and shared top-8, B in {1,2,4,8}",
-    "cfg3": "262144-row N(0,1) cache, B=1, 2048 uniform + 128 pads",
-    "cfg4": "262144-row Student-t cache, B=8, locality-biased, 0-256 pads",
-    "cfg5": "prefill-shaped T=2048 over the Student-t cache; 2048 scattered writes",
+    "rows16384_b1": "16384-row cache, B=1, 2048 uniform + 128 pads",
+    "moe_align_b1_b8": "MoE align, distinct top-8 and shared top-8, B in {1,2,4,8}",
+    "rows262144_normal_b1": "262144-row N(0,1) cache, B=1, 2048 uniform + 128 pads",
+    "rows262144_t3_b8": "262144-row Student-t cache, B=8, locality-biased, 0-256 pads",
+    "prefill_t2048": "prefill-shaped T=2048 over the Student-t cache; 2048 scattered writes",
 }
 
 
@@ -38,7 +38,7 @@ def summary_lines():
     lines = []
     if not ATTENTION and not EXACT:
         return lines
-    lines.append("north_star bars: bf16 attention max-abs <= 2e-2 and mean-abs <= 2e-3 against the oracle; "
+    lines.append("parity bars: bf16 attention max-abs <= 2e-2 and mean-abs <= 2e-3 against the oracle; "
                  "cache rows and MoE align outputs bit-exact")
     for cfg, desc in CONFIGS.items():
         ex = [r for r in EXACT if r["config"] == cfg]

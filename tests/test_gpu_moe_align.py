@@ -63,7 +63,7 @@ def test_distinct_topk_and_adversarial(cuda, oracle):
         for case, routes in (("distinct top-8", ids), ("shared top-8", shared)):
             want = oracle.moe_align(routes.cpu().numpy())
             got = [t.cpu().numpy() for t in titan_moe_align_small(routes)]
-            record_exact("cfg2", f"MoE align {case} (sorted_ids, expert_ids, padded count)",
+            record_exact("moe_align_b1_b8", f"MoE align {case} (sorted_ids, expert_ids, padded count)",
                          sum(int(np.count_nonzero(a != b)) if a.shape == b.shape else a.size
                              for a, b in zip(got, want)), sum(b.size for b in want))
             if case == "shared top-8":

@@ -92,7 +92,7 @@ def test_small_b1_splits(cuda, oracle, small_cache, splits):
     torch.cuda.synchronize()
     want = oracle.sparse_mla(u16(w["q"]), rows, w["idx"].cpu().numpy(), W.SM_SCALE, n_splits=splits,
                              groups=kernel_groups(w["idx"].shape[-1], splits), block_n=BLOCK, lazy=LAZY)
-    mx, mean = compare(out, want, f"splits={splits}", config="cfg1")
+    mx, mean = compare(out, want, f"splits={splits}", config="rows16384_b1")
     assert mean < 1e-4        # ~bf16 ulp-level agreement
 
 
@@ -319,7 +319,7 @@ def test_full_context_b1_b8(cuda, oracle, full_cache):
             want = oracle.sparse_mla(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE, n_splits=s,
                                      nthreads=oracle.default_threads(), groups=kernel_groups(idx.shape[-1], s),
                                      block_n=BLOCK, lazy=LAZY)
-            compare(out, want, (name, splits), config="cfg4" if name == "b8" else None)
+            compare(out, want, (name, splits), config="rows262144_t3_b8" if name == "b8" else None)
             ref64 = oracle.sparse_mla_f64(u16(q), rows, idx.cpu().numpy(), W.SM_SCALE,
                                           nthreads=oracle.default_threads())
             textbook_check(out, ref64, (name, splits))
@@ -344,7 +344,7 @@ def test_prefill_shaped_sampled(cuda, oracle, full_cache):
     want = oracle.sparse_mla(qs, rows, ids, W.SM_SCALE, n_splits=1, nthreads=oracle.default_threads(),
                              groups=kernel_groups(idx.shape[-1], 1), block_n=BLOCK, lazy=LAZY)
     got = out[torch.as_tensor(pick, device=cuda)]
-    compare(got, want, "prefill sample", config="cfg5")
+    compare(got, want, "prefill sample", config="prefill_t2048")
 
 
 # ---------------------------------------------------------------- the reference's own reduction
@@ -382,7 +382,7 @@ def test_reference_reduction_small(cuda, oracle, small_cache):
             "reference splits": triton_mla_sparse_attention(w["q"], kv, w["idx"], W.SM_SCALE,
                                                             num_kv_splits=ref_splits(1))}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, w["q"], rows, w["idx"], "small B1", config="cfg1")
+    check_reference_reduction(oracle, outs, w["q"], rows, w["idx"], "small B1", config="rows16384_b1")
 
 
 @pytest.fixture(scope="module")
@@ -409,7 +409,7 @@ def test_reference_reduction_full_b1(cuda, oracle, normal_cache):
     outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE),
             "reference splits": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=ref_splits(1))}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, q, rows, idx, "full B1", config="cfg3")
+    check_reference_reduction(oracle, outs, q, rows, idx, "full B1", config="rows262144_normal_b1")
 
 
 @pytest.mark.slow
@@ -425,7 +425,7 @@ def test_reference_reduction_full_b8(cuda, oracle, full_cache):
     outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE),
             "reference splits": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE, num_kv_splits=ref_splits(8))}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, q, rows, idx, "full B8", config="cfg4")
+    check_reference_reduction(oracle, outs, q, rows, idx, "full B8", config="rows262144_t3_b8")
 
 
 @pytest.mark.slow
@@ -442,7 +442,7 @@ def test_reference_reduction_prefill_all_tokens(cuda, oracle, full_cache):
     log_case("mla prefill-shaped T=2048, all tokens, vs the reference reduction")
     outs = {"auto": triton_mla_sparse_attention(q, kv, idx, W.SM_SCALE)}
     torch.cuda.synchronize()
-    check_reference_reduction(oracle, outs, q, rows, idx, "prefill T=2048", config="cfg5")
+    check_reference_reduction(oracle, outs, q, rows, idx, "prefill T=2048", config="prefill_t2048")
 
 
 def test_merge_beyond_register_splits(cuda, oracle, small_cache):

@@ -26,7 +26,7 @@ def test_writer_small_bit_exact(cuda, oracle):
     torch.cuda.synchronize()
     got = u8(w["cache"]).reshape(-1, 528)
     want = oracle.quantize_rows(u16(w["x"]), nthreads=oracle.default_threads())
-    record_exact("cfg1", "store_int8 rows (bytes)", np.count_nonzero(got != want), got.size)
+    record_exact("rows16384_b1", "store_int8 rows (bytes)", np.count_nonzero(got != want), got.size)
     assert np.array_equal(got, want)
 
 
@@ -150,7 +150,7 @@ def test_full_context_writer_bit_exact(cuda, oracle):
         torch.cuda.synchronize()
         got = u8(cache).reshape(-1, 528)
         want = oracle.quantize_rows(u16(x), nthreads=oracle.default_threads())
-        record_exact("cfg3" if dist == "normal" else "cfg4", "store_int8 rows (bytes)",
+        record_exact("rows262144_normal_b1" if dist == "normal" else "rows262144_t3_b8", "store_int8 rows (bytes)",
                      np.count_nonzero(got != want), got.size)
         assert np.array_equal(got, want), dist
         del x, cache
@@ -177,8 +177,8 @@ def test_prefill_scattered_writer_full_size(cuda, oracle):
     want = oracle.quantize_rows(u16(new_rows), nthreads=oracle.default_threads())
     untouched = np.ones(flat.shape[0], bool)
     untouched[s] = False
-    record_exact("cfg5", "store_int8 scattered rows (bytes)", np.count_nonzero(flat[s] != want), want.size)
-    record_exact("cfg5", "rows not written (bytes changed)", np.count_nonzero(flat[untouched] != was[untouched]),
+    record_exact("prefill_t2048", "store_int8 scattered rows (bytes)", np.count_nonzero(flat[s] != want), want.size)
+    record_exact("prefill_t2048", "rows not written (bytes changed)", np.count_nonzero(flat[untouched] != was[untouched]),
                  flat[untouched].size)
     assert np.array_equal(flat[s], want)
     assert np.array_equal(flat[untouched], was[untouched])

@@ -17,15 +17,15 @@ def clean_log(monkeypatch):
 
 def test_summary_lines(clean_log):
     want = np.array([0.5, -1.0, 2.5, 5.0] * 64, np.float32)
-    mla_bar.check_bar(want + np.float32(1e-3), want, "small", config="cfg1")
+    mla_bar.check_bar(want + np.float32(1e-3), want, "small", config="rows16384_b1")
     flip = want.copy()
     flip[3] = 5.03125            # one bf16 ulp above 5.0: over 2e-2, within the exception
-    mla_bar.check_bar(flip, want, "flip", config="cfg4")
-    parity_log.record_exact("cfg2", "MoE align", 0, 96)
+    mla_bar.check_bar(flip, want, "flip", config="rows262144_t3_b8")
+    parity_log.record_exact("moe_align_b1_b8", "MoE align", 0, 96)
     lines = parity_log.summary_lines()
     text = "\n".join(lines)
-    assert "cfg1 attention" in text and "literal bar held by 1" in text
-    assert "cfg2 MoE align: 0 of 96 differ" in text
+    assert "rows16384_b1 attention" in text and "literal bar held by 1" in text
+    assert "moe_align_b1_b8 MoE align: 0 of 96 differ" in text
     assert "all attention comparisons: 2; the literal bar (flat max-abs 2e-2, mean-abs 2e-3) held by 1" in text
     assert "[flip]: max-abs 0.03125, 1 of 256 elements over 2e-2, at most 1 bf16 ulp" in text
 
