@@ -1,6 +1,6 @@
 """GPU parity of triton_mla_sparse_attention (HIP) against the CPU oracle.
 
-Bar (BF16 attention output), the north-star one: mean-abs <= 2e-3 and per
+Bar (BF16 attention output), the target one: mean-abs <= 2e-3 and per
 element |err| <= 2e-2, where rare elements with |ref| >= 2 may differ by up to
 two bf16 ulps of the reference value instead (rounding flips; see compare),
 against
