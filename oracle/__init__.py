@@ -382,15 +382,75 @@ def moe_w4a16(x_u16: np.ndarray, w13: np.ndarray, s13: np.ndarray, w2: np.ndarra
     c3 = 0.  Returns (out bf16 bits [T, K], c2 bf16 bits [T*topk, N] with
     zero rows for dropped routes).  `cache` (a dict, optional) keeps the
     dequantised experts between calls on the same weights."""
-    L = np.float32(np.inf if clamp_limit is None else clamp_limit)
+    cache = {} if cache is None else cache
+    c1 = moe_w4a16_c1(x_u16, w13, s13, w2, s2, topk_ids, cache)
+    act = f32_to_bf16(moe_activation(c1, clamp_limit))
+    routed = ((np.asarray(topk_ids) >= 0) & (np.asarray(topk_ids) < w13.shape[0])).reshape(-1)
+    act[~routed] = 0
+    out, _ = moe_w4a16_down(act, w13, s13, w2, s2, topk_weights, topk_ids, cache)
+    return out, act
+
+
+def moe_w4a16_c1(x_u16: np.ndarray, w13: np.ndarray, s13: np.ndarray, w2: np.ndarray, s2: np.ndarray,
+                 topk_ids: np.ndarray, cache: dict | None = None, with_magnitude: bool = False):
+    """c1 = bf16(x . W13^T) (exact float64 dot) of every route as float32
+    [T*topk, 2N] (gate then up), row t * topk + j; zero rows for routes whose
+    expert is outside [0, E).  with_magnitude: also return, per output,
+    280 * sum_k |s_k x_k| (s_k the group scale of feature k): the size of
+    the partial sums an fp32 evaluation on biased codes passes through
+    ((128 + q) codes and a -136 seed: |128 + q| + 136 <= 280), which scales
+    its rounding error when the result itself is small."""
     x = bf16_to_f32(x_u16).astype(np.float64)
     E = w13.shape[0]
-    N = w13.shape[1] // 2
     T, topk = topk_ids.shape
-    K = x.shape[1]
+    ids = np.asarray(topk_ids, dtype=np.int64)
+    c1 = np.zeros((T * topk, w13.shape[1]), dtype=np.float32)
+    mag = np.zeros_like(c1)
+    cache = {} if cache is None else cache
+    for t in range(T):
+        for j in range(topk):
+            e = int(ids[t, j])
+            if 0 <= e < E:
+                W13 = _experts(cache, e, w13, s13, w2, s2)[0].astype(np.float64)
+                c1[t * topk + j] = bf16_to_f32(f32_to_bf16((W13 @ x[t]).astype(np.float32)))
+                if with_magnitude:
+                    s = np.abs(bf16_to_f32(s13[e]).astype(np.float64))          # [2N, K/32]
+                    xs = np.abs(x[t]).reshape(-1, 32).sum(axis=1)                # [K/32]
+                    mag[t * topk + j] = 280.0 * (s @ xs)
+    return (c1, mag) if with_magnitude else c1
+
+
+def moe_activation(c1: np.ndarray, clamp_limit: float | None = 10.0) -> np.ndarray:
+    """silu(min(g, L)) * clip(u, -L, L) in fp32 for c1 rows [..., 2N] (gate
+    then up); returns fp32 [..., N] before the bf16 rounding."""
+    L = np.float32(np.inf if clamp_limit is None else clamp_limit)
+    N = c1.shape[-1] // 2
+    g = np.minimum(c1[..., :N].astype(np.float32), L)
+    u = np.clip(c1[..., N:].astype(np.float32), -L, L)
+    with np.errstate(over="ignore"):
+        return (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32)
+
+
+def _experts(cache: dict, e: int, w13, s13, w2, s2):
+    """Expert e's dequantised (W13, W2) in fp32, kept in `cache`; (q - 8) * s
+    is exact in fp32 (a 4-bit code times a bf16 scale)."""
+    if e not in cache:
+        cache[e] = (_dequant(w13[e], s13[e]).astype(np.float32), _dequant(w2[e], s2[e]).astype(np.float32))
+    return cache[e]
+
+
+def moe_w4a16_down(act_u16: np.ndarray, w13: np.ndarray, s13: np.ndarray, w2: np.ndarray, s2: np.ndarray,
+                   topk_weights: np.ndarray, topk_ids: np.ndarray, cache: dict | None = None):
+    """The layer's second half on given activations c2 (bf16 bits [T*topk, N],
+    row t * topk + j): c3 = bf16(fp32(w) * fp32(c2 . W2^T)) with an exact
+    float64 dot, out = bf16 of the fp32 sum of the token's c3 in slot order;
+    a route whose expert is outside [0, E) gives c3 = 0.  Returns (out bf16
+    bits [T, K], c3 float32 [T, topk, K])."""
+    E = w2.shape[0]
+    K = w2.shape[1]
+    T, topk = topk_ids.shape
     ids = np.asarray(topk_ids, dtype=np.int64)
     tw = np.asarray(topk_weights, dtype=np.float32)
-    act = np.zeros((T * topk, N), dtype=np.uint16)
     c3 = np.zeros((T, topk, K), dtype=np.float32)
     cache = {} if cache is None else cache
     for t in range(T):
@@ -398,23 +458,13 @@ def moe_w4a16(x_u16: np.ndarray, w13: np.ndarray, s13: np.ndarray, w2: np.ndarra
             e = int(ids[t, j])
             if not 0 <= e < E:
                 continue
-            if e not in cache:   # (q - 8) * s is exact in fp32 (4-bit code times bf16 scale)
-                cache[e] = (_dequant(w13[e], s13[e]).astype(np.float32),
-                            _dequant(w2[e], s2[e]).astype(np.float32))
-            W13, W2 = (m.astype(np.float64) for m in cache[e])
-            c1 = bf16_to_f32(f32_to_bf16((W13 @ x[t]).astype(np.float32)))
-            g = np.minimum(c1[:N], L)
-            u = np.clip(c1[N:], -L, L)
-            with np.errstate(over="ignore"):
-                c2 = g / (np.float32(1) + np.exp(-g)) * u
-            c2b = f32_to_bf16(c2.astype(np.float32))
-            act[t * topk + j] = c2b
-            y = (W2 @ bf16_to_f32(c2b).astype(np.float64)).astype(np.float32)
+            W2 = _experts(cache, e, w13, s13, w2, s2)[1].astype(np.float64)
+            y = (W2 @ bf16_to_f32(act_u16[t * topk + j]).astype(np.float64)).astype(np.float32)
             c3[t, j] = bf16_to_f32(f32_to_bf16(tw[t, j] * y))
     out = np.zeros((T, K), dtype=np.float32)
     for j in range(topk):
         out += c3[:, j]
-    return f32_to_bf16(out), act
+    return f32_to_bf16(out), c3
 
 
 # --------------------------------------------------------------------------
