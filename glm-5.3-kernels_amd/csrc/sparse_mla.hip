@@ -37,6 +37,13 @@
 //   * V^T comes from the same gathered rows: each wave stores its bf16 slice
 //     row-major in LDS and reads it back with ds_read_b64_tr_b16 (two reads
 //     per 16x32 operand).  O^T accumulates in 8 MFMA tiles per wave.
+//   * Splits longer than one chunk (the prefill-shaped call's single split
+//     of 2176 keys per token) run sparse_mla_pair_kernel instead: two waves
+//     per (token, 16-head group) share one online-softmax stream over the
+//     split's tiles in order.
+//   * Workgroups are numbered so that a token's splits share an XCD (its L2
+//     holds the token's q and indices, and the merge kernel is numbered the
+//     same way); see sparse_mla_kernel.
 #include "glm53_common.h"
 
 #include <atomic>
