@@ -851,7 +851,6 @@ def main():
                              "hbm_frac_layer_rotation": round(mb / (us_rot * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)}
             del calls
         extra["moe_w4a16_layer"] = moew
-        del layers
 
         # ------------------------------------------------------------ sparse indexer (decode)
         # FP8 paged MQA logits of each request's 65536 pools (262144-token
@@ -892,6 +891,70 @@ def main():
             idx[f"B{b}"] = row
             del sets, q_i, cache_i, w_i, lens_i, bt_i, logits_i
         extra["indexer_decode"] = idx
+
+        # ------------------------------------------------------------ one decode layer's path, B=8
+        # The path's rows composed as one layer of a B=8 decode step (8
+        # requests at 262144 tokens sharing one 262144-row cache, the headline
+        # shape): the 8 new latents written (store_int8), the indexer's
+        # logits + top-512 pools, the pooled attention (expansion, page
+        # mapping and split-KV in one launch, then the merge) and the fused
+        # W4A16 MoE layer.  4 layers of their own caches, pool caches and
+        # expert weights cycled in a graph of 16 steps (≈ 1.1 GB read per
+        # cycle of 4: HBM), against the same components' graphs alone over the
+        # same layers.
+        from titan_mla import triton_mla_sparse_attention_pooled
+        gl = W.gen(dev, W.SEED_BENCH + 500)
+        lay_path = []
+        for li in range(4):
+            _, xl, cl, sl = W.decode_cache(dev, seed=W.SEED_BENCH + 500 + li, dist="t3")
+            store_int8(xl, cl, sl)
+            del xl, sl
+            iset = W.indexer_decode_inputs(dev, gl, batch=8)
+            xm, idm, twm = W.moe_w4a16_inputs(8, dev, gl)
+            lay_path.append((cl, iset, (xm, idm, twm, layers[li])))
+        pages = n_rows // W.BLOCK
+        bt_path = torch.arange(pages, dtype=torch.int32, device=dev).repeat(8, 1).contiguous()
+        req_path = torch.arange(8, dtype=torch.int32, device=dev)
+        q_path = torch.randn(8, 16, 512, generator=gl, device=dev).to(torch.bfloat16)
+        x_new = torch.randn(8, 512, generator=gl, device=dev).to(torch.bfloat16)
+        slots_path = torch.randperm(n_rows, generator=gl, device=dev)[:8]
+
+        def write(lp):
+            store_int8(x_new, lp[0], slots_path)
+
+        def index(lp):
+            return indexer_decode_pool_topk(*lp[1])
+
+        def attend(lp, pools_l):
+            seq_l = lp[1][3] * W.INDEX_KPOOL          # complete pools: no tail
+            return triton_mla_sparse_attention_pooled(q_path, lp[0], pools_l, seq_l, W.INDEX_KPOOL, req_path,
+                                                      bt_path, W.SM_SCALE, topk=W.TOPK)
+
+        def moe(lp):
+            c = lp[2]
+            return fused_moe_w4a16(c[0], c[3][0], c[3][2], c[3][1], c[3][3], c[2], c[1])
+
+        pools_pre = [index(lp) for lp in lay_path]      # the attention-alone graph's inputs
+        cyc = 4                                         # the 4 layers 4 times: 16 steps per graph
+        parts = {"store_int8": lambda: [write(lp) for _ in range(cyc) for lp in lay_path],
+                 "indexer_logits_topk": lambda: [index(lp) for _ in range(cyc) for lp in lay_path],
+                 "pooled_attention": lambda: [attend(lp, p) for _ in range(cyc) for lp, p in zip(lay_path, pools_pre)],
+                 "moe_w4a16_layer": lambda: [moe(lp) for _ in range(cyc) for lp in lay_path],
+                 "layer": lambda: [(write(lp), attend(lp, index(lp)), moe(lp)) for _ in range(cyc) for lp in lay_path]}
+        path = {}
+        log("decode layer path B=8 (write + indexer + pooled attention + MoE), 4 layers")
+        for name, fn in parts.items():
+            gpth, _ = capture(torch, fn, 1)
+            for _ in range(3):
+                gpth.replay()
+            path[f"us_{name}"] = round(timer.replay_loop(gpth, max(4, K // 8)) / (cyc * len(lay_path)), 2)
+            del gpth
+        path["us_sum_of_parts"] = round(sum(v for k, v in path.items() if k != "us_layer"), 2)
+        path["what"] = ("per layer, B=8 decode over 262144-token contexts: store_int8 of 8 rows, indexer logits "
+                        "over 65536 pools + top-512, pooled sparse MLA (2176 slots), fused W4A16 MoE; 4 layers "
+                        "cycled 4 times in one graph of 16 steps, each component alone the same way")
+        extra["decode_layer_path_b8"] = path
+        del lay_path, pools_pre, layers
 
         # ------------------------------------------------------------ sparse indexer (prefill shape)
         # The reference's TP4 prefill indexer benchmark, replicated branch on
