@@ -286,14 +286,17 @@ def test_nan_token_propagates(cuda, oracle, moe):
     assert_out_close(out[keep], want[keep], oracle, "tokens without NaN")
 
 
-def test_graph_replay_deterministic(cuda, moe):
+@pytest.mark.parametrize("batch", [1, 8])
+def test_graph_replay_deterministic(cuda, moe, batch):
+    """Graph replays equal the eager call (B=1 takes the one-token gate/up
+    path, B=8 the aligned blocks)."""
     import torch
     from titan_moe_w4a16 import fused_moe_w4a16
     g = torch.Generator(device=cuda).manual_seed(93)
-    x, ids, tw = W.moe_w4a16_inputs(8, cuda, g)
+    x, ids, tw = W.moe_w4a16_inputs(batch, cuda, g)
     d = moe["dev"]
     fn = lambda: fused_moe_w4a16(x, d["w13"], d["w2"], d["w13_scale"], d["w2_scale"], tw, ids)
-    log_case("fused moe graph capture B=8")
+    log_case("fused moe graph capture", batch)
     eager = fn()
     again = fn()
     torch.cuda.synchronize()
